@@ -1,0 +1,162 @@
+/*
+ * sllm_qmm.h — C ABI of the MI355X (gfx950) quantized-matmul library that
+ * replaces scriptling-llm-lib's int8 matmul path.
+ *
+ * Every entry point names the reference function it stands in for
+ * (paths relative to the reference repository root). All functions return an
+ * sllm_status; on failure sllm_last_error() gives a message for the calling
+ * thread. Nothing here aborts the process, and no entry point falls back to a
+ * CPU path: a missing GPU is an error (SLLM_ERR_DEVICE).
+ *
+ * Threading: weight handles are immutable after creation and may be shared by
+ * any number of threads; every matmul call is independent (the host-pointer
+ * entry points draw a private HIP stream and staging buffers from a pool).
+ *
+ * Layout conventions (same as the reference): x is xRows x xCols fp32
+ * row-major, dst is xRows x rows fp32 row-major (dst[xi*rows + j]), weights
+ * are [rows][cols/32 blocks] with rows = GGUF Dims[1], cols = Dims[0].
+ */
+#ifndef SLLM_QMM_H
+#define SLLM_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    SLLM_OK = 0,
+    SLLM_ERR_ARG = 1,         /* null pointer, bad size, shape mismatch */
+    SLLM_ERR_QTYPE = 2,       /* QType / GGUF type this path does not take */
+    SLLM_ERR_SHAPE = 3,       /* cols not a multiple of the block size, or beyond limits */
+    SLLM_ERR_DEVICE = 4,      /* no usable gfx950 device, or a HIP runtime error */
+    SLLM_ERR_OOM = 5,         /* device or pinned-host allocation failed */
+    SLLM_ERR_FORMAT = 6       /* Raw bytes not in the form the QType requires */
+} sllm_status;
+
+/* QType of a weight, as in QuantWeight.QType (gguf.go:73-79). */
+typedef enum {
+    SLLM_Q8_0 = 0,  /* "q8"   34 B / 32: f16 d, int8 q[32]                          */
+    SLLM_Q4_0 = 1,  /* "q4"   18 B / 32: f16 d, 16 nibble bytes, w = d*(nib-8)        */
+    SLLM_Q4_1 = 2,  /* "q4_1" 20 B / 32: f16 d, f16 m, 16 nibble bytes, w = d*nib+m   */
+    SLLM_Q5_0 = 3,  /* "q5"   22 B / 32: f16 d, u32 qh, 16 nibble bytes, w = d*(q5-16)*/
+    SLLM_Q5K1 = 4   /* "q5k1" Q5_K as two summed Q4_1 tensors (kquant_kernels.go:103-154) */
+} sllm_qtype;
+
+typedef struct sllm_weight sllm_weight;
+
+/* Library set-up on the current HIP device; idempotent. Optional: every other
+ * entry point initialises on first use. */
+sllm_status sllm_init(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char *sllm_last_error(void);
+
+/* Static description: arch, plane layout version, kernel configuration. */
+const char *sllm_kernel_info(void);
+
+/* --------------------------------------------------------------------------
+ * Weight creation (load time). Each call repacks the block bytes once into
+ * HBM-resident planes: quant plane(s), f16 scale plane, f16 min plane (Q4_1,
+ * Q5K1), high-bit plane (Q5_0, Q5K1). The call is synchronous.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * From a QuantWeight as the reference holds it (gguf.go:73-79): qtype is the
+ * QType string ("q8", "q4", "q4_1", "q5", "q5k1"), raw/raw_bytes its Raw bytes
+ * in host memory, groups/rows/cols its fields. Replaces keeping QuantWeight.Raw
+ * on the host for modelMatmulQuantIntoF32 (float32_ops.go:379).
+ * "q5k1" Raw must be what convertQ5KToTwoQ41 produces (high half: min 0 and
+ * 0/1 nibbles), else SLLM_ERR_FORMAT.
+ */
+sllm_status sllm_weight_from_quant(const char *qtype, const void *raw, size_t raw_bytes,
+                                   int groups, int rows, int cols, sllm_weight **out);
+
+/*
+ * From a GGUF tensor (type id and its block bytes in host memory): the
+ * int8-kernel branches of loadWeightF32Direct (gguf.go:818-934), run on the GPU.
+ *   8 Q8_0, 2 Q4_0, 3 Q4_1, 6 Q5_0: repacked as is;
+ *   12 Q4_K -> Q4_1 (convertQ4KToQ41, kquant_kernels.go:30-63);
+ *   13 Q5_K -> Q5K1 (convertQ5KToTwoQ41, kquant_kernels.go:110-154);
+ *   14 Q6_K, 20 IQ4_NL -> Q8_0 (dequantize in fp64 + quantizeQ8Rows,
+ *      gguf.go:889-894,912-921,979-1015,1080-1134).
+ * Other types return SLLM_ERR_QTYPE (the reference's dense-fp32 branch).
+ */
+sllm_status sllm_weight_from_gguf(uint32_t ggml_type, const void *raw, size_t raw_bytes,
+                                  int rows, int cols, sllm_weight **out);
+
+/*
+ * From dense fp32 weights (host memory, rows x cols): Q8_0 via
+ * quantizeQ8RowsF32 (gguf.go:1136-1186), as the tied output head is built
+ * (model_f32.go:150-152).
+ */
+sllm_status sllm_weight_from_f32(const float *w, int rows, int cols, sllm_weight **out);
+
+void sllm_weight_destroy(sllm_weight *w);
+
+/* QuantWeight fields of a handle. */
+sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int *rows, int *cols,
+                             size_t *raw_bytes);
+
+/*
+ * Rebuild the reference Raw bytes (QuantWeight.Raw layout) from the device
+ * planes into host memory (cap >= raw_bytes). Bit-exact inverse of the repack.
+ */
+sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap);
+
+/* --------------------------------------------------------------------------
+ * Matmul (decode GEMV for xRows < 64 tokens, int8-MFMA GEMM for xRows >= 64).
+ * ------------------------------------------------------------------------ */
+
+/*
+ * modelMatmulQuantIntoF32 (float32_ops.go:379-460) for a handle: host x and
+ * dst, synchronous (dst is filled when it returns). Covers q8q8MatmulInto
+ * (q8q8.go:147), q4q8MatmulInto (q4q8.go:49), q41q8MatmulInto (q41q8.go:20),
+ * q5k1MatmulInto (kquant_kernels.go:159) and the Q5_0 branch (:427-436).
+ */
+sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int x_rows, int x_cols,
+                                       float *dst);
+
+/* modelMatmulRowQuantIntoF32 (float32_ops.go:620-707): one activation row. */
+sllm_status sllm_matmul_row_quant_into_f32(const sllm_weight *w, const float *normed, float *dst);
+
+/*
+ * Device-resident variant: x and dst are device pointers, work is enqueued on
+ * `stream` (a hipStream_t; NULL = the default stream) and the call returns
+ * without synchronising. May allocate device scratch on first use of a larger
+ * shape (GEMM activation workspace).
+ */
+sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x_dev, int x_rows, int x_cols,
+                            float *dst_dev, void *stream);
+
+/* argmaxF32 (float32_ops.go:812-822) over n device floats; result to host. */
+sllm_status sllm_argmax_dev(const float *v_dev, int n, int *out, void *stream);
+
+/* --------------------------------------------------------------------------
+ * Verification entry points (bit-exact checks; not on the hot path).
+ * ------------------------------------------------------------------------ */
+
+/* quantizeActivationsQ8 (q8q8.go:96-125) on the GPU, with the same device
+ * routine the matmul prologue uses. Host buffers: x [rows*cols], xq
+ * [rows*cols], xs [rows*cols/32], sum_xq [rows*cols/32] (may be NULL). */
+sllm_status sllm_debug_quantize_act(const float *x, int rows, int cols, int8_t *xq, float *xs,
+                                    int32_t *sum_xq);
+
+/*
+ * Per-(activation row, weight row, block) integer dots computed by the same
+ * device block routines as the matmul: out is int32 [x_rows][rows][groups]
+ * (x2 in the last dimension for Q5K1: low, high). For Q5_0 (fp32 activations)
+ * each entry is the fp32 in-block partial sum's bit pattern.
+ */
+sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_rows, int x_cols,
+                                  int32_t *out);
+
+/* Tuning knob for launch-shape sweeps ("gemv_grid_cap", "gemv_waves"...). */
+sllm_status sllm_set_param(const char *name, int value);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

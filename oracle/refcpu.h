@@ -1,0 +1,104 @@
+/*
+ * refcpu — scalar CPU restatement of scriptling-llm-lib's quantized-matmul
+ * arithmetic, used ONLY as a test oracle and as the CPU baseline in bench.py.
+ *
+ * TEST INFRASTRUCTURE. Nothing in the product library links, loads or calls
+ * this code; only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may use it, and then only as the checker / the timed CPU baseline.
+ *
+ * Every function cites the reference file:line whose arithmetic it restates
+ * (paths relative to the reference repository root). Semantics that matter for
+ * bit-exactness are reproduced literally: operation order, float32 vs float64
+ * evaluation, truncation vs rounding, and the f16 decode each path uses.
+ * The file must be compiled with -ffp-contract=off and without fast-math.
+ */
+#ifndef SLLM_REFCPU_H
+#define SLLM_REFCPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- f16 codecs -------------------------------------------------------- */
+float    ref_f16_to_f32_lut(uint16_t h);    /* dot_scalar.go:46-64 (f16LUT q8q8.go:52,60-62) */
+float    ref_f16_to_f32_cvtph(uint16_t h);  /* VCVTPH2PS semantics, q4q8_row_amd64.s:36-38 */
+double   ref_f16_to_f64(uint16_t h);        /* llm_primitives.go:698-717 */
+uint16_t ref_f64_to_f16(double f);          /* quantize.go:133-159 */
+
+/* ---- quantizers -------------------------------------------------------- */
+/* q8q8.go:96-125: per-32-block absmax, scale=maxAbs/127, q=trunc(x*inv) */
+void ref_quantize_act_q8(const float *x, int groups, int8_t *q, float *s);
+/* gguf.go:1136-1186 (fp32 weights -> Q8_0 raw, 34 B/block). returns 0 on ok */
+int ref_quantize_q8_rows_f32(const float *w, int rows, int cols, uint8_t *out);
+/* gguf.go:1080-1134 (fp64 weights -> Q8_0 raw). returns 0 on ok */
+int ref_quantize_q8_rows_f64(const double *w, int rows, int cols, uint8_t *out);
+
+/* ---- dequantizers (fp64, as the loader computes them) -------------------- */
+void ref_dequant_q8_0(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:424-435 */
+void ref_dequant_q4_0(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:437-452 */
+void ref_dequant_q4_1(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:454-470 */
+void ref_dequant_q5_0(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:472-490 */
+void ref_dequant_q4_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.go:73-102 */
+void ref_dequant_q5_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.go:104-145 */
+void ref_dequant_q6_k(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:979-1015 */
+void ref_dequant_iq4_nl(const uint8_t *raw, int64_t n, double *out);/* kquants.go:7-27 */
+
+/* ---- load-time remaps / requantization ---------------------------------- */
+void ref_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m); /* kquants.go:62-71 */
+/* kquant_kernels.go:30-63: Q4_K rows -> Q4_1 rows (rows*cols/32*20 bytes) */
+void ref_convert_q4k_to_q41(const uint8_t *src, int rows, int cols, uint8_t *out);
+/* kquant_kernels.go:110-154: Q5_K rows -> [low Q4_1 half][high Q4_1 half] */
+void ref_convert_q5k_to_two_q41(const uint8_t *src, int rows, int cols, uint8_t *out);
+/*
+ * gguf.go:818-934 (loadWeightF32Direct, the int8-kernel branches): turns a
+ * GGUF tensor of type ggml_type into the QuantWeight the matmul consumes.
+ * Writes the QType name into qtype (>= 8 bytes) and the Raw bytes into out
+ * (capacity out_cap). Returns Raw size in bytes, or -1 for a type the int8
+ * path does not take (the reference then builds a dense fp32 weight).
+ */
+int64_t ref_load_weight(uint32_t ggml_type, const uint8_t *raw, int rows, int cols,
+                        char *qtype, uint8_t *out, int64_t out_cap);
+
+/* ---- integer block dots -------------------------------------------------- */
+int32_t ref_int8_dot(const int8_t *a, const int8_t *b, int n); /* q8q8.go:83-91 */
+/*
+ * Per-(activation row m, weight row n, block g) integer block dots as the
+ * reference's kernels form them (see ref_block_dots in refcpu.c for each
+ * format's definition). Output int32 [M][N][G] (x2 for q5k1: [..][G][2]);
+ * for q5 the fp32 in-block partial sum (before the d scale) is written as
+ * its bit pattern. Returns 0, or -1 for an unknown qtype.
+ */
+int ref_block_dots(const char *qtype, const uint8_t *raw, int N, int G,
+                   const int8_t *xq, const float *x, int M, int32_t *out);
+
+/* ---- row dots (one weight row x one quantized activation row) ---------- */
+float ref_q8q8_row(const uint8_t *w, const int8_t *xq, const float *xs, int groups);      /* q8q8.go:131-141, q8q8_row_amd64.s:16-58 */
+float ref_q4q8_row(const uint8_t *w, const int8_t *xq, const float *xs, int groups);      /* q4q8.go:29-45 (d via VCVTPH2PS) */
+float ref_q41q8_row(const uint8_t *w, const int8_t *xq, const float *xs, const int32_t *sum_xq, int groups); /* q41q8_row_amd64.s:25-83 */
+float ref_q5_row(const uint8_t *w, const float *x, int groups);                           /* float32_ops.go:335-367,507-513 */
+
+/* ---- matmul drivers (dst[xi*N + j]) -------------------------------------- */
+void ref_q8q8_matmul(const uint8_t *raw, int N, int G, const float *x, int M, float *dst);  /* q8q8.go:147-246 */
+void ref_q4q8_matmul(const uint8_t *raw, int N, int G, const float *x, int M, float *dst);  /* q4q8.go:49-101 */
+void ref_q41q8_matmul(const uint8_t *raw, int N, int G, const float *x, int M, float *dst); /* q41q8.go:20-60 */
+void ref_q5k1_matmul(const uint8_t *raw, int N, int G, const float *x, int M, float *dst);  /* kquant_kernels.go:159-174 */
+void ref_q5_matmul(const uint8_t *raw, int N, int G, const float *x, int M, float *dst);    /* float32_ops.go:427-436 */
+/*
+ * float32_ops.go:379-460 (modelMatmulQuantIntoF32) dispatch on QType.
+ * Returns 0, or -1 for an unknown qtype (the reference then leaves dst unfilled).
+ */
+int ref_matmul_quant(const char *qtype, const uint8_t *raw, int N, int K,
+                     const float *x, int M, float *dst);
+/* float32_ops.go:812-822: first index of the maximum (strict >). */
+int ref_argmax(const float *v, int n);
+
+/* Bytes per 32-element block of a QType's Raw ("q5k1" counts both halves). */
+int ref_block_bytes(const char *qtype);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,505 @@
+// C ABI (include/sllm_qmm.h): weight handles, the matmul entry points that
+// stand in for the reference's Go matmul functions, and verification hooks.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "qmm_internal.hpp"
+
+struct sllm_weight {
+    int fmt = 0;
+    int groups = 0, rows = 0, cols = 0;
+    int device = 0;
+    void *base = nullptr;
+    size_t bytes = 0;
+    sllm::MutPlanes planes;
+};
+
+namespace sllm {
+
+namespace {
+
+thread_local std::string g_err;
+
+std::mutex g_mu;
+bool g_init_done = false;
+sllm_status g_init_status = SLLM_ERR_DEVICE;
+std::string g_init_msg;
+
+// Per-call resources for the host-pointer entry points: a stream and device
+// staging buffers, pooled so concurrent callers never share one.
+struct Ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    void *buf = nullptr;
+    size_t cap = 0;
+};
+std::vector<Ctx *> g_pool;
+
+// GEMM activation workspace per (device, stream), grown on demand.
+struct Ws {
+    void *p = nullptr;
+    size_t cap = 0;
+};
+std::unordered_map<uint64_t, Ws> g_ws;
+
+sllm_status ensure_init() {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_init_done) {
+        if (g_init_status != SLLM_OK) return set_error(g_init_status, g_init_msg);
+        return SLLM_OK;
+    }
+    g_init_done = true;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        g_init_status = SLLM_ERR_DEVICE;
+        g_init_msg = "no HIP device available (this library needs an MI355X / gfx950 GPU)";
+        return set_error(g_init_status, g_init_msg);
+    }
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, dev);
+    if (e != hipSuccess) {
+        g_init_status = SLLM_ERR_DEVICE;
+        g_init_msg = std::string("hipGetDeviceProperties: ") + hipGetErrorString(e);
+        return set_error(g_init_status, g_init_msg);
+    }
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        g_init_status = SLLM_ERR_DEVICE;
+        g_init_msg = std::string("device is ") + prop.gcnArchName + ", this build targets gfx950 only";
+        return set_error(g_init_status, g_init_msg);
+    }
+    g_init_status = SLLM_OK;
+    return SLLM_OK;
+}
+
+sllm_status acquire(Ctx **out, size_t bytes) {
+    int dev = 0;
+    SLLM_HIP(hipGetDevice(&dev));
+    Ctx *c = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        for (size_t i = 0; i < g_pool.size(); i++) {
+            if (g_pool[i]->device == dev) {
+                c = g_pool[i];
+                g_pool.erase(g_pool.begin() + (long)i);
+                break;
+            }
+        }
+    }
+    if (!c) {
+        c = new Ctx();
+        c->device = dev;
+        hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            delete c;
+            return hip_error(e, "hipStreamCreateWithFlags");
+        }
+    }
+    if (c->cap < bytes) {
+        if (c->buf) (void)hipFree(c->buf);
+        c->buf = nullptr;
+        c->cap = 0;
+        size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        hipError_t e = hipMalloc(&c->buf, want);
+        if (e != hipSuccess) {
+            std::lock_guard<std::mutex> lk(g_mu);
+            g_pool.push_back(c);
+            return set_error(SLLM_ERR_OOM, "device staging allocation failed");
+        }
+        c->cap = want;
+    }
+    *out = c;
+    return SLLM_OK;
+}
+
+void release(Ctx *c) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_pool.push_back(c);
+}
+
+int parse_qtype(const char *q) {
+    if (!q) return -1;
+    if (!std::strcmp(q, "q8")) return SLLM_Q8_0;
+    if (!std::strcmp(q, "q4")) return SLLM_Q4_0;
+    if (!std::strcmp(q, "q4_1")) return SLLM_Q4_1;
+    if (!std::strcmp(q, "q5")) return SLLM_Q5_0;
+    if (!std::strcmp(q, "q5k1")) return SLLM_Q5K1;
+    return -1;
+}
+
+sllm_status alloc_weight(int fmt, int rows, int cols, sllm_weight **out) {
+    auto *w = new sllm_weight();
+    w->fmt = fmt;
+    w->rows = rows;
+    w->cols = cols;
+    w->groups = cols / 32;
+    (void)hipGetDevice(&w->device);
+    const int64_t nb = (int64_t)rows * w->groups;
+    w->bytes = carve_planes(fmt, nb, nullptr, nullptr);
+    hipError_t e = hipMalloc(&w->base, w->bytes);
+    if (e != hipSuccess) {
+        delete w;
+        return set_error(SLLM_ERR_OOM, "weight plane allocation failed");
+    }
+    carve_planes(fmt, nb, w->base, &w->planes);
+    *out = w;
+    return SLLM_OK;
+}
+
+// Upload `bytes` of host memory into the context buffer and run `fn` on it.
+template <class F>
+sllm_status with_upload(const void *host, size_t bytes, size_t extra, F fn) {
+    Ctx *c = nullptr;
+    sllm_status st = acquire(&c, bytes + extra + 256);
+    if (st != SLLM_OK) return st;
+    hipError_t e = hipMemcpyAsync(c->buf, host, bytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = fn(c);
+        if (st == SLLM_OK) e = hipStreamSynchronize(c->stream);
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "upload");
+    return st;
+}
+
+bool check_shape(int rows, int cols, sllm_status *st) {
+    if (rows <= 0 || cols <= 0) {
+        *st = set_error(SLLM_ERR_ARG, "rows and cols must be positive");
+        return false;
+    }
+    if (cols % 32) {
+        *st = set_error(SLLM_ERR_SHAPE, "cols must be a multiple of 32");
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+sllm_status set_error(sllm_status st, const std::string &msg) {
+    g_err = msg;
+    return st;
+}
+
+sllm_status hip_error(hipError_t e, const char *what) {
+    g_err = std::string(what) + ": " + hipGetErrorString(e);
+    return SLLM_ERR_DEVICE;
+}
+
+Tuning &tuning() {
+    static Tuning t;
+    return t;
+}
+
+}  // namespace sllm
+
+using namespace sllm;
+
+extern "C" {
+
+sllm_status sllm_init(void) { return ensure_init(); }
+
+const char *sllm_last_error(void) { return g_err.c_str(); }
+
+const char *sllm_kernel_info(void) {
+    static std::string info;
+    const Tuning &t = tuning();
+    char buf[512];
+    std::snprintf(buf, sizeof buf,
+                  "sllm_qmm gfx950 planes-v1 | gemv: %d waves/WG, grid cap %d, K-split to >=%d batches, "
+                  "fused Q8_0 LDS prologue | gemm: int8 MFMA from xRows>=%d",
+                  t.gemv_waves, t.gemv_grid_cap, t.gemv_min_batches, t.gemm_min_rows);
+    info = buf;
+    return info.c_str();
+}
+
+sllm_status sllm_set_param(const char *name, int value) {
+    if (!name) return set_error(SLLM_ERR_ARG, "null name");
+    Tuning &t = tuning();
+    if (!std::strcmp(name, "gemv_grid_cap") && value >= 1) t.gemv_grid_cap = value;
+    else if (!std::strcmp(name, "gemv_waves") && (value == 4 || value == 8 || value == 16)) t.gemv_waves = value;
+    else if (!std::strcmp(name, "gemv_min_batches") && value >= 1) t.gemv_min_batches = value;
+    else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
+    else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_from_quant(const char *qtype, const void *raw, size_t raw_bytes, int groups, int rows,
+                                   int cols, sllm_weight **out) {
+    if (!out || !raw) return set_error(SLLM_ERR_ARG, "null pointer");
+    *out = nullptr;
+    const int fmt = parse_qtype(qtype);
+    if (fmt < 0) return set_error(SLLM_ERR_QTYPE, std::string("unknown QType ") + (qtype ? qtype : "(null)"));
+    sllm_status st = SLLM_OK;
+    if (!check_shape(rows, cols, &st)) return st;
+    if (groups != cols / 32) return set_error(SLLM_ERR_ARG, "groups must equal cols/32");
+    const size_t need = (size_t)rows * groups * raw_block_bytes(fmt);
+    if (raw_bytes < need) return set_error(SLLM_ERR_ARG, "Raw is shorter than rows*groups blocks");
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    sllm_weight *w = nullptr;
+    if ((st = alloc_weight(fmt, rows, cols, &w)) != SLLM_OK) return st;
+    int flag = 0;
+    st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
+        int *err = (int *)((char *)c->buf + ((need + 255) & ~(size_t)255));
+        SLLM_HIP(hipMemsetAsync(err, 0, sizeof(int), c->stream));
+        sllm_status s2 = pack_from_raw(fmt, (const uint8_t *)c->buf, rows, groups, w->planes, err, c->stream);
+        if (s2 != SLLM_OK) return s2;
+        SLLM_HIP(hipMemcpyAsync(&flag, err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+        return SLLM_OK;
+    });
+    if (st == SLLM_OK && flag)
+        st = set_error(SLLM_ERR_FORMAT, "q5k1 high half is not in convertQ5KToTwoQ41 form (min 0, 0/1 nibbles)");
+    if (st != SLLM_OK) {
+        sllm_weight_destroy(w);
+        return st;
+    }
+    *out = w;
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes, int rows, int cols,
+                                  sllm_weight **out) {
+    if (!out || !raw) return set_error(SLLM_ERR_ARG, "null pointer");
+    *out = nullptr;
+    sllm_status st = SLLM_OK;
+    if (!check_shape(rows, cols, &st)) return st;
+    int fmt = -1;
+    size_t per = 0, blk = 32;
+    switch (t) {
+    case 8: fmt = SLLM_Q8_0; per = 34; break;
+    case 2: fmt = SLLM_Q4_0; per = 18; break;
+    case 3: fmt = SLLM_Q4_1; per = 20; break;
+    case 6: fmt = SLLM_Q5_0; per = 22; break;
+    case 12: fmt = SLLM_Q4_1; per = 144; blk = 256; break;
+    case 13: fmt = SLLM_Q5K1; per = 176; blk = 256; break;
+    case 14: fmt = SLLM_Q8_0; per = 210; blk = 256; break;
+    case 20: fmt = SLLM_Q8_0; per = 18; break;
+    default:
+        return set_error(SLLM_ERR_QTYPE, "GGUF type " + std::to_string(t) +
+                                             " has no int8 kernel (the reference loads it as dense fp32)");
+    }
+    if (cols % blk) return set_error(SLLM_ERR_SHAPE, "cols must be a multiple of the super-block size 256");
+    const size_t need = (size_t)rows * (cols / blk) * per;
+    if (raw_bytes < need) return set_error(SLLM_ERR_ARG, "raw is shorter than the tensor's blocks");
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    sllm_weight *w = nullptr;
+    if ((st = alloc_weight(fmt, rows, cols, &w)) != SLLM_OK) return st;
+    st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
+        const uint8_t *dev = (const uint8_t *)c->buf;
+        if (t == 8 || t == 2 || t == 3 || t == 6) return pack_from_raw(fmt, dev, rows, cols / 32, w->planes, nullptr, c->stream);
+        return pack_from_gguf(t, dev, rows, cols, w->planes, c->stream);
+    });
+    if (st != SLLM_OK) {
+        sllm_weight_destroy(w);
+        return st;
+    }
+    *out = w;
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_from_f32(const float *wf, int rows, int cols, sllm_weight **out) {
+    if (!out || !wf) return set_error(SLLM_ERR_ARG, "null pointer");
+    *out = nullptr;
+    sllm_status st = SLLM_OK;
+    if (!check_shape(rows, cols, &st)) return st;
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    sllm_weight *w = nullptr;
+    if ((st = alloc_weight(SLLM_Q8_0, rows, cols, &w)) != SLLM_OK) return st;
+    st = with_upload(wf, (size_t)rows * cols * sizeof(float), 0, [&](Ctx *c) -> sllm_status {
+        return pack_from_f32((const float *)c->buf, rows, cols, w->planes, c->stream);
+    });
+    if (st != SLLM_OK) {
+        sllm_weight_destroy(w);
+        return st;
+    }
+    *out = w;
+    return SLLM_OK;
+}
+
+void sllm_weight_destroy(sllm_weight *w) {
+    if (!w) return;
+    if (w->base) (void)hipFree(w->base);
+    delete w;
+}
+
+sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int *rows, int *cols,
+                             size_t *raw_bytes) {
+    if (!w) return set_error(SLLM_ERR_ARG, "null weight");
+    if (qtype) *qtype = w->fmt;
+    if (groups) *groups = w->groups;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (raw_bytes) *raw_bytes = (size_t)w->rows * w->groups * raw_block_bytes(w->fmt);
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap) {
+    if (!w || !raw) return set_error(SLLM_ERR_ARG, "null pointer");
+    const int64_t nb = (int64_t)w->rows * w->groups;
+    const size_t need = (size_t)nb * raw_block_bytes(w->fmt);
+    if (cap < need) return set_error(SLLM_ERR_ARG, "export buffer too small");
+    std::vector<unsigned char> img(w->bytes);
+    SLLM_HIP(hipMemcpy(img.data(), w->base, w->bytes, hipMemcpyDeviceToHost));
+    MutPlanes p;
+    carve_planes(w->fmt, nb, img.data(), &p);
+    unsigned char *o = (unsigned char *)raw;
+    auto put16 = [](unsigned char *dst, uint16_t v) { dst[0] = (unsigned char)v; dst[1] = (unsigned char)(v >> 8); };
+    for (int64_t b = 0; b < nb; b++) {
+        switch (w->fmt) {
+        case SLLM_Q8_0:
+            put16(o + b * 34, p.d[b]);
+            std::memcpy(o + b * 34 + 2, &p.qs[b], 16);
+            std::memcpy(o + b * 34 + 18, &p.qs2[b], 16);
+            break;
+        case SLLM_Q4_0:
+            put16(o + b * 18, p.d[b]);
+            std::memcpy(o + b * 18 + 2, &p.qs[b], 16);
+            break;
+        case SLLM_Q4_1:
+            put16(o + b * 20, p.d[b]);
+            put16(o + b * 20 + 2, p.m[b]);
+            std::memcpy(o + b * 20 + 4, &p.qs[b], 16);
+            break;
+        case SLLM_Q5_0:
+            put16(o + b * 22, p.d[b]);
+            std::memcpy(o + b * 22 + 2, &p.qh[b], 4);
+            std::memcpy(o + b * 22 + 6, &p.qs[b], 16);
+            break;
+        case SLLM_Q5K1: {
+            unsigned char *lo = o + b * 20, *hi = o + (nb + b) * 20;
+            put16(lo, p.d[b]);
+            put16(lo + 2, p.m[b]);
+            std::memcpy(lo + 4, &p.qs[b], 16);
+            put16(hi, p.dh[b]);
+            put16(hi + 2, 0);
+            for (int i = 0; i < 16; i++)
+                hi[4 + i] = (unsigned char)(((p.qh[b] >> i) & 1u) | (((p.qh[b] >> (i + 16)) & 1u) << 4));
+            break;
+        }
+        }
+    }
+    return SLLM_OK;
+}
+
+sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, int x_cols, float *dst,
+                            void *stream) {
+    if (!w || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (x_cols != w->cols) return set_error(SLLM_ERR_ARG, "xCols does not match the weight's Cols");
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    Planes P = as_const(w->planes);
+    return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+}
+
+sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int x_rows, int x_cols, float *dst) {
+    if (!w || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (x_cols != w->cols) return set_error(SLLM_ERR_ARG, "xCols does not match the weight's Cols");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    const size_t xb = (size_t)x_rows * x_cols * sizeof(float);
+    const size_t yb = (size_t)x_rows * w->rows * sizeof(float);
+    const size_t yoff = (xb + 255) & ~(size_t)255;
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, yoff + yb)) != SLLM_OK) return st;
+    float *dx = (float *)c->buf;
+    float *dy = (float *)((char *)c->buf + yoff);
+    hipError_t e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = sllm_matmul_dev(w, dx, x_rows, x_cols, dy, c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(dst, dy, yb, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "matmul transfer");
+    return st;
+}
+
+sllm_status sllm_matmul_row_quant_into_f32(const sllm_weight *w, const float *normed, float *dst) {
+    if (!w) return set_error(SLLM_ERR_ARG, "null weight");
+    return sllm_matmul_quant_into_f32(w, normed, 1, w->cols, dst);
+}
+
+sllm_status sllm_argmax_dev(const float *v, int n, int *out, void *stream) {
+    if (!v || !out || n <= 0) return set_error(SLLM_ERR_ARG, "bad argument");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, 256)) != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    st = launch_argmax(v, n, (int *)c->buf, s);
+    hipError_t e = hipSuccess;
+    if (st == SLLM_OK) {
+        e = hipMemcpyAsync(out, c->buf, sizeof(int), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "argmax");
+    return st;
+}
+
+sllm_status sllm_debug_quantize_act(const float *x, int rows, int cols, int8_t *xq, float *xs, int32_t *sum_xq) {
+    if (!x || !xq || !xs) return set_error(SLLM_ERR_ARG, "null pointer");
+    sllm_status st = SLLM_OK;
+    if (!check_shape(rows, cols, &st)) return st;
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    const int G = cols / 32;
+    const size_t xb = (size_t)rows * cols * 4, qb = (size_t)rows * cols, sb = (size_t)rows * G * 4;
+    const size_t oq = (xb + 255) & ~(size_t)255, os = oq + ((qb + 255) & ~(size_t)255), ox = os + ((sb + 255) & ~(size_t)255);
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, ox + sb)) != SLLM_OK) return st;
+    char *b = (char *)c->buf;
+    hipError_t e = hipMemcpyAsync(b, x, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = launch_quantize_act((float *)b, rows, G, (int8_t *)(b + oq), (float *)(b + os), (int32_t *)(b + ox), c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(xq, b + oq, qb, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipMemcpyAsync(xs, b + os, sb, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess && sum_xq) e = hipMemcpyAsync(sum_xq, b + ox, sb, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "debug_quantize_act");
+    return st;
+}
+
+sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_rows, int x_cols, int32_t *out) {
+    if (!w || !x || !out) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0 || x_cols != w->cols) return set_error(SLLM_ERR_ARG, "bad activation shape");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    const size_t xb = (size_t)x_rows * x_cols * 4;
+    const size_t ob = (size_t)x_rows * w->rows * w->groups * 4 * (w->fmt == SLLM_Q5K1 ? 2 : 1);
+    const size_t oo = (xb + 255) & ~(size_t)255;
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, oo + ob)) != SLLM_OK) return st;
+    char *b = (char *)c->buf;
+    hipError_t e = hipMemcpyAsync(b, x, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = launch_block_dots(w->fmt, as_const(w->planes), (const float *)b, w->rows, w->groups, x_rows,
+                               (int32_t *)(b + oo), c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(out, b + oo, ob, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "debug_block_dots");
+    return st;
+}
+
+}  // extern "C"

@@ -1,0 +1,173 @@
+// Device-side building blocks shared by the GEMV, GEMM and verification kernels:
+// f16 codecs, the bit-exact Q8_0 activation quantizer and the per-block integer
+// dots of each weight format. Compiled with -ffp-contract=off: every float
+// expression below rounds each operation separately, in the order written,
+// which is the order the reference evaluates it in.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace sllm {
+
+// ------------------------------------------------------------------ f16 ----
+
+// Exact IEEE half -> float (v_cvt_f32_f16; f16 denormals are kept). This is the
+// decode the reference's fused Q4_0 / Q4_1 kernels perform with VCVTPH2PS
+// (q4q8_row_amd64.s:36-38, q41q8_row_amd64.s:58-63).
+__device__ __forceinline__ float f16_exact(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// The reference's table decode f16ToF32 / f16LUT (dot_scalar.go:46-64,
+// q8q8.go:60-62), used for Q8_0 and Q5_0 scales: identical to the exact decode
+// except that every f16 subnormal becomes a signed zero (the Go code divides a
+// float32 denormal by 2^24, which underflows).
+__device__ __forceinline__ float f16_lut(uint16_t h) {
+    float f = f16_exact(h);
+    return (h & 0x7c00u) ? f : __builtin_copysignf(0.0f, f);
+}
+
+// float64ToFloat16 (quantize.go:133-159): NaN/Inf -> 0, mantissa truncated,
+// values below the f16 normal range flush to a signed zero.
+__device__ __forceinline__ uint16_t f64_to_f16_trunc(double f) {
+    uint64_t bits = __builtin_bit_cast(uint64_t, f);
+    uint64_t exp64 = (bits >> 52) & 0x7ffu;
+    if (exp64 == 0x7ffu) return 0;  // NaN or Inf
+    uint16_t sign = (uint16_t)((bits >> 48) & 0x8000u);
+    if (exp64 == 0) return sign;
+    int exp16 = (int)exp64 - 1023 + 15;
+    if (exp16 <= 0) return sign;
+    if (exp16 >= 0x1f) return sign | 0x7c00u;
+    return sign | (uint16_t)(exp16 << 10) | (uint16_t)((bits >> 42) & 0x3ffu);
+}
+
+// ------------------------------------------------- activation quantizer ----
+
+// Go's int32(float32) on amd64 (CVTTSS2SL) followed by the clamp of
+// quantizeActivationsQ8: truncation toward zero; NaN, +-Inf and values outside
+// int32 become INT32_MIN and so clamp to -128.
+__device__ __forceinline__ int quant_trunc_clamp(float p) {
+    int q = (p >= -2147483648.0f && p < 2147483648.0f) ? (int)p : INT32_MIN;
+    q = q > 127 ? 127 : q;
+    q = q < -128 ? -128 : q;
+    return q;
+}
+
+// One quarter of a 32-element block (4 consecutive fp32 values held by one of
+// the 8 lanes that share the block; the 8 lanes are consecutive and aligned).
+// Returns the 4 int8 codes packed little-endian; *scale and *sum receive the
+// block's fp32 scale and Σq in every lane of the 8. q8q8.go:96-125.
+__device__ __forceinline__ uint32_t quantize_quarter(float4 v, float *scale, int *sum) {
+    float a = 0.0f, t;
+    t = __builtin_fabsf(v.x); a = t > a ? t : a;
+    t = __builtin_fabsf(v.y); a = t > a ? t : a;
+    t = __builtin_fabsf(v.z); a = t > a ? t : a;
+    t = __builtin_fabsf(v.w); a = t > a ? t : a;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) {
+        float o = __shfl_xor(a, off);
+        a = o > a ? o : a;
+    }
+    float s = 0.0f, inv = 0.0f;
+    if (a > 0.0f) {
+        s = a / 127.0f;
+        inv = 1.0f / s;
+    }
+    int q0 = quant_trunc_clamp(v.x * inv);
+    int q1 = quant_trunc_clamp(v.y * inv);
+    int q2 = quant_trunc_clamp(v.z * inv);
+    int q3 = quant_trunc_clamp(v.w * inv);
+    int sm = q0 + q1 + q2 + q3;
+#pragma unroll
+    for (int off = 1; off < 8; off <<= 1) sm += __shfl_xor(sm, off);
+    *scale = s;
+    *sum = sm;
+    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
+           ((uint32_t)(q3 & 0xff) << 24);
+}
+
+// ---------------------------------------------------------- block dots ----
+
+__device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+// Σ w·xq over a Q8_0 block: w halves (elements 0..15, 16..31), xq halves likewise.
+__device__ __forceinline__ int q8_isum(int4 wl, int4 wh, int4 xl, int4 xh) {
+    int s = dot4(wl.x, xl.x, 0);
+    s = dot4(wl.y, xl.y, s);
+    s = dot4(wl.z, xl.z, s);
+    s = dot4(wl.w, xl.w, s);
+    s = dot4(wh.x, xh.x, s);
+    s = dot4(wh.y, xh.y, s);
+    s = dot4(wh.z, xh.z, s);
+    s = dot4(wh.w, xh.w, s);
+    return s;
+}
+
+// Σ nib·xq over a 4-bit block (16 GGUF nibble bytes: low nibbles are elements
+// 0..15, high nibbles 16..31).
+__device__ __forceinline__ int nib_isum(int4 q, int4 xl, int4 xh) {
+    const int lo = 0x0f0f0f0f;
+    int s = dot4(q.x & lo, xl.x, 0);
+    s = dot4(q.y & lo, xl.y, s);
+    s = dot4(q.z & lo, xl.z, s);
+    s = dot4(q.w & lo, xl.w, s);
+    s = dot4((q.x >> 4) & lo, xh.x, s);
+    s = dot4((q.y >> 4) & lo, xh.y, s);
+    s = dot4((q.z >> 4) & lo, xh.z, s);
+    s = dot4((q.w >> 4) & lo, xh.w, s);
+    return s;
+}
+
+// Four bits (b0..b3 of t) -> four bytes holding 0 or 1.
+__device__ __forceinline__ int spread4(uint32_t t) { return (int)(((t & 0xfu) * 0x00204081u) & 0x01010101u); }
+
+// Σ bit_e·xq_e for a 32-bit mask (bit e = element e): the Q5K1 high block.
+__device__ __forceinline__ int bits_isum(uint32_t hb, int4 xl, int4 xh) {
+    int s = dot4(spread4(hb), xl.x, 0);
+    s = dot4(spread4(hb >> 4), xl.y, s);
+    s = dot4(spread4(hb >> 8), xl.z, s);
+    s = dot4(spread4(hb >> 12), xl.w, s);
+    s = dot4(spread4(hb >> 16), xh.x, s);
+    s = dot4(spread4(hb >> 20), xh.y, s);
+    s = dot4(spread4(hb >> 24), xh.z, s);
+    s = dot4(spread4(hb >> 28), xh.w, s);
+    return s;
+}
+
+// Q5_0 in-block fp32 partial sum in the reference order (q5DotGroupXF32,
+// float32_ops.go:335-367): sum += v0*x[j] + v1*x[j+16] for j = 0..15, with
+// v = float(q5) - 16 and q5 = nibble | (bit e of qh) << 4. xb holds the block's
+// 32 activations (8 float4).
+__device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 *xb) {
+    const uint32_t w[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
+    float sum = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        float4 a = xb[jj];      // elements 4jj .. 4jj+3
+        float4 b = xb[jj + 4];  // elements 16+4jj ..
+        const float av[4] = {a.x, a.y, a.z, a.w};
+        const float bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            int j = 4 * jj + k;
+            uint32_t byte = (w[jj] >> (8 * k)) & 0xffu;
+            int q0 = (int)((byte & 0x0fu) | (((qh >> j) & 1u) << 4));
+            int q1 = (int)((byte >> 4) | (((qh >> (j + 16)) & 1u) << 4));
+            float v0 = (float)q0 - 16.0f;
+            float v1 = (float)q1 - 16.0f;
+            float p0 = v0 * av[k];
+            float p1 = v1 * bv[k];
+            float pair = p0 + p1;
+            sum = sum + pair;
+        }
+    }
+    return sum;
+}
+
+// Padded LDS stride (floats) of one 32-element fp32 activation block, chosen so
+// that 16 lanes reading 16 B from consecutive blocks hit distinct banks.
+constexpr int kXfStride = 36;
+
+}  // namespace sllm

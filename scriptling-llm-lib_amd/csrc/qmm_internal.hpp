@@ -1,0 +1,113 @@
+// Host-side definitions shared by the library's translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "sllm_qmm.h"
+
+namespace sllm {
+
+// Device planes of one weight. Every plane is [rows][groups] in block order,
+// rows contiguous, each plane 256-byte aligned inside one allocation.
+//   qs   16 B / block: Q8_0 elements 0..15 (int8); Q4_0 / Q4_1 / Q5_0 / Q5K1 the
+//        16 GGUF nibble bytes (byte i = element i low nibble | element i+16 high)
+//   qs2  16 B / block: Q8_0 elements 16..31
+//   d    f16 scale bits           (all formats)
+//   m    f16 min bits             (Q4_1, Q5K1 low block)
+//   dh   f16 scale of the Q5K1 high block (16 * d*sc, truncated separately)
+//   qh   u32 high bits, bit e = bit 4 of element e (Q5_0, Q5K1)
+struct Planes {
+    const int4 *qs = nullptr;
+    const int4 *qs2 = nullptr;
+    const uint16_t *d = nullptr;
+    const uint16_t *m = nullptr;
+    const uint16_t *dh = nullptr;
+    const uint32_t *qh = nullptr;
+};
+
+struct MutPlanes {
+    int4 *qs = nullptr;
+    int4 *qs2 = nullptr;
+    uint16_t *d = nullptr;
+    uint16_t *m = nullptr;
+    uint16_t *dh = nullptr;
+    uint32_t *qh = nullptr;
+};
+
+// Bytes each format streams per 32-element block from the planes.
+inline int plane_block_bytes(int fmt) {
+    switch (fmt) {
+    case SLLM_Q8_0: return 34;
+    case SLLM_Q4_0: return 18;
+    case SLLM_Q4_1: return 20;
+    case SLLM_Q5_0: return 22;
+    case SLLM_Q5K1: return 26;
+    }
+    return 0;
+}
+
+// Bytes per block of the reference Raw layout (QuantWeight.Raw).
+inline int raw_block_bytes(int fmt) {
+    switch (fmt) {
+    case SLLM_Q8_0: return 34;
+    case SLLM_Q4_0: return 18;
+    case SLLM_Q4_1: return 20;
+    case SLLM_Q5_0: return 22;
+    case SLLM_Q5K1: return 40;
+    }
+    return 0;
+}
+
+// Carve the planes of a (rows x groups) weight of format fmt out of `base`
+// (nullptr: only compute the size). Returns the total allocation size.
+size_t carve_planes(int fmt, int64_t nblocks, void *base, MutPlanes *out);
+
+inline Planes as_const(const MutPlanes &p) {
+    Planes c;
+    c.qs = p.qs; c.qs2 = p.qs2; c.d = p.d; c.m = p.m; c.dh = p.dh; c.qh = p.qh;
+    return c;
+}
+
+// Thread-local error message plumbing.
+sllm_status set_error(sllm_status st, const std::string &msg);
+sllm_status hip_error(hipError_t e, const char *what);
+
+#define SLLM_HIP(call)                                             \
+    do {                                                           \
+        hipError_t e_ = (call);                                    \
+        if (e_ != hipSuccess) return ::sllm::hip_error(e_, #call); \
+    } while (0)
+
+// Kernel launch helpers implemented in the .hip files.
+sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                        hipStream_t s);
+sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                        void *ws, size_t ws_bytes, hipStream_t s);
+size_t gemm_workspace_bytes(int fmt, int N, int G, int M);
+sllm_status launch_quantize_act(const float *x, int rows, int G, int8_t *xq, float *xs, int32_t *sx,
+                                hipStream_t s);
+sllm_status launch_block_dots(int fmt, const Planes &P, const float *x, int N, int G, int M,
+                              int32_t *out, hipStream_t s);
+sllm_status launch_argmax(const float *v, int n, int *out_dev, hipStream_t s);
+
+// Weight creation kernels: raw (device) -> planes.
+sllm_status pack_from_raw(int fmt, const uint8_t *raw_dev, int rows, int G, const MutPlanes &P,
+                          int *err_flag_dev, hipStream_t s);
+sllm_status pack_from_gguf(uint32_t ggml_type, const uint8_t *raw_dev, int rows, int cols,
+                           const MutPlanes &P, hipStream_t s);
+sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
+
+// Tuning parameters (launch shapes), settable through sllm_set_param.
+struct Tuning {
+    int gemv_grid_cap = 1024;  // max workgroups of a GEMV launch
+    int gemv_waves = 8;        // waves per GEMV workgroup (4, 8 or 16)
+    int gemv_min_batches = 512;// split K until at least this many row batches
+    int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
+};
+Tuning &tuning();
+
+}  // namespace sllm

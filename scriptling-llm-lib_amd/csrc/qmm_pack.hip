@@ -1,0 +1,304 @@
+// Load-time weight preparation on the GPU: GGUF / QuantWeight block bytes ->
+// HBM planes. One thread per output 32-element block. Covers the repack of
+// native blocks and the remaps the reference performs in gguf.go:818-934:
+//   Q4_K -> Q4_1            (convertQ4KToQ41, kquant_kernels.go:30-63)
+//   Q5_K -> two Q4_1 halves (convertQ5KToTwoQ41, kquant_kernels.go:110-154)
+//   Q6_K, IQ4_NL -> Q8_0    (fp64 dequant gguf.go:988-1015 / kquants.go:14-27,
+//                            then quantizeQ8Rows gguf.go:1080-1134)
+//   fp32 -> Q8_0            (quantizeQ8RowsF32, gguf.go:1136-1186)
+// All arithmetic is the reference's: fp64 products (exact for these inputs),
+// IEEE fp64/fp32 division, round-half-away-from-zero, truncating f16 encode.
+#include <hip/hip_runtime.h>
+
+#include "qmm_device.hpp"
+#include "qmm_internal.hpp"
+
+namespace sllm {
+
+size_t carve_planes(int fmt, int64_t nb, void *base, MutPlanes *out) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> void * {
+        off = (off + 255) & ~(size_t)255;
+        void *p = base ? (void *)((char *)base + off) : nullptr;
+        off += bytes;
+        return p;
+    };
+    MutPlanes p;
+    p.qs = (int4 *)take((size_t)nb * 16);
+    if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take((size_t)nb * 16);
+    if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take((size_t)nb * 4);
+    p.d = (uint16_t *)take((size_t)nb * 2);
+    if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1) p.m = (uint16_t *)take((size_t)nb * 2);
+    if (fmt == SLLM_Q5K1) p.dh = (uint16_t *)take((size_t)nb * 2);
+    if (out) *out = p;
+    return (off + 255) & ~(size_t)255;
+}
+
+namespace {
+
+__device__ __forceinline__ uint16_t ld16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+__device__ __forceinline__ int4 ld_int4(const uint8_t *p) {
+    int4 v;
+    v.x = (int)ld32(p);
+    v.y = (int)ld32(p + 4);
+    v.z = (int)ld32(p + 8);
+    v.w = (int)ld32(p + 12);
+    return v;
+}
+__device__ __forceinline__ double f16_to_f64(uint16_t h) { return (double)f16_exact(h); }
+
+// Go's byte(int8(f64)) on amd64 (CVTTSD2SL, low byte): NaN -> 0.
+__device__ __forceinline__ uint32_t f64_to_i8_byte(double v) {
+    if (!(v >= -2147483648.0 && v < 2147483648.0)) return 0;
+    return (uint32_t)(int8_t)(int32_t)v & 0xffu;
+}
+
+// quantizeQ8Rows (gguf.go:1098-1125) for one block of 32 fp64 values.
+__device__ void q8_from_f64(const double *v, int4 &lo, int4 &hi, uint16_t &d) {
+    double maxAbs = 0.0;
+    for (int i = 0; i < 32; i++) {
+        double a = __builtin_fabs(v[i]);
+        if (a > maxAbs) maxAbs = a;
+    }
+    double scale = 0.0;
+    if (maxAbs > 0) scale = maxAbs / 127.0;
+    d = f64_to_f16_trunc(scale);
+    const double inv = 1.0 / scale;
+    uint32_t w[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < 32; i++) {
+        double val = v[i] * inv;
+        if (val > 127) val = 127;
+        else if (val < -128) val = -128;
+        w[i >> 2] |= f64_to_i8_byte(round(val)) << (8 * (i & 3));
+    }
+    lo = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+    hi = make_int4((int)w[4], (int)w[5], (int)w[6], (int)w[7]);
+}
+
+// getScaleMinK4 (kquants.go:62-71).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t *q, int &sc, int &m) {
+    if (j < 4) {
+        sc = q[j] & 63;
+        m = q[j + 4] & 63;
+    } else {
+        sc = (q[j + 4] & 0x0f) | ((q[j - 4] >> 6) << 4);
+        m = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+// Sub-block jj of a Q4_K / Q5_K super-block as a Q4_1 block (kquant_kernels.go:41-59).
+__device__ __forceinline__ void kquant_low_block(const uint8_t *sb, const uint8_t *qs, int jj, int4 &q,
+                                                 uint16_t &d, uint16_t &m, double &dsc) {
+    const double dd = f16_to_f64(ld16(sb));
+    const double dmin = f16_to_f64(ld16(sb + 2));
+    int sc, mm;
+    scale_min_k4(jj, sb + 4, sc, mm);
+    dsc = dd * (double)sc;
+    d = f64_to_f16_trunc(dsc);
+    m = f64_to_f16_trunc((-dmin) * (double)mm);
+    const int k = (jj / 2) * 32;
+    uint32_t w[4] = {0, 0, 0, 0};
+    for (int i = 0; i < 16; i++) {
+        uint32_t b = (jj & 1) ? (uint32_t)((qs[k + i] >> 4) | ((qs[k + i + 16] >> 4) << 4))
+                              : (uint32_t)((qs[k + i] & 0x0f) | ((qs[k + i + 16] & 0x0f) << 4));
+        w[i >> 2] |= (b & 0xffu) << (8 * (i & 3));
+    }
+    q = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
+}
+
+// Native QuantWeight.Raw blocks -> planes. For q5k1 the Raw is [low][high];
+// the high half must be in the form convertQ5KToTwoQ41 writes (min 0, 0/1
+// nibbles), otherwise *err is set.
+__global__ void pack_raw_kernel(int fmt, const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P,
+                                int *__restrict__ err) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        switch (fmt) {
+        case SLLM_Q8_0: {
+            const uint8_t *p = raw + b * 34;
+            P.d[b] = ld16(p);
+            P.qs[b] = ld_int4(p + 2);
+            P.qs2[b] = ld_int4(p + 18);
+            break;
+        }
+        case SLLM_Q4_0: {
+            const uint8_t *p = raw + b * 18;
+            P.d[b] = ld16(p);
+            P.qs[b] = ld_int4(p + 2);
+            break;
+        }
+        case SLLM_Q4_1: {
+            const uint8_t *p = raw + b * 20;
+            P.d[b] = ld16(p);
+            P.m[b] = ld16(p + 2);
+            P.qs[b] = ld_int4(p + 4);
+            break;
+        }
+        case SLLM_Q5_0: {
+            const uint8_t *p = raw + b * 22;
+            P.d[b] = ld16(p);
+            P.qh[b] = ld32(p + 2);
+            P.qs[b] = ld_int4(p + 6);
+            break;
+        }
+        case SLLM_Q5K1: {
+            const uint8_t *lo = raw + b * 20;
+            const uint8_t *hi = raw + (nb + b) * 20;
+            P.d[b] = ld16(lo);
+            P.m[b] = ld16(lo + 2);
+            P.qs[b] = ld_int4(lo + 4);
+            P.dh[b] = ld16(hi);
+            uint32_t bits = 0;
+            bool bad = ld16(hi + 2) != 0;
+            for (int i = 0; i < 16; i++) {
+                uint32_t v = hi[4 + i];
+                bad |= (v & 0xeeu) != 0;
+                bits |= (v & 1u) << i;
+                bits |= ((v >> 4) & 1u) << (i + 16);
+            }
+            P.qh[b] = bits;
+            if (bad) *err = 1;
+            break;
+        }
+        }
+    }
+}
+
+// Q4_K (144 B / 256) -> Q4_1 planes; block b = (row, super-block, jj).
+__global__ void pack_q4k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 144;
+        double dsc;
+        kquant_low_block(sb, sb + 16, (int)(b & 7), P.qs[b], P.d[b], P.m[b], dsc);
+    }
+}
+
+// Q5_K (176 B / 256) -> Q5K1 planes (low Q4_1 block + high-bit block).
+__global__ void pack_q5k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 176;
+        const int jj = (int)(b & 7);
+        double dsc;
+        kquant_low_block(sb, sb + 48, jj, P.qs[b], P.d[b], P.m[b], dsc);
+        P.dh[b] = f64_to_f16_trunc(16 * dsc);
+        const uint8_t *qh = sb + 16;
+        uint32_t bits = 0;
+        for (int i = 0; i < 16; i++) {
+            bits |= (uint32_t)((qh[i] >> jj) & 1) << i;
+            bits |= (uint32_t)((qh[i + 16] >> jj) & 1) << (i + 16);
+        }
+        P.qh[b] = bits;
+    }
+}
+
+// Q6_K (210 B / 256) -> Q8_0 planes. Q8 block b of a super-block covers
+// elements 32*(b%8) ..: half n = (b%8)/4, quarter k = (b%8)%4 of dequantizeQ6KBlock.
+__global__ void pack_q6k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 210;
+        const int j = (int)(b & 7), n = j >> 2, k = j & 3;
+        const double d = f16_to_f64(ld16(sb + 208));
+        const uint8_t *ql = sb + n * 64 + (k & 1) * 32;
+        const uint8_t *qh = sb + 128 + n * 32;
+        const uint8_t *sc = sb + 192 + n * 8 + 2 * k;
+        double v[32];
+        for (int l = 0; l < 32; l++) {
+            int nib = (k < 2) ? (ql[l] & 0x0f) : (ql[l] >> 4);
+            int q = (int)(int8_t)(nib | (((qh[l] >> (2 * k)) & 3) << 4)) - 32;
+            double s = (double)(int8_t)sc[l / 16];
+            v[l] = d * s * (double)q;
+        }
+        int4 lo, hi;
+        uint16_t dd;
+        q8_from_f64(v, lo, hi, dd);
+        P.qs[b] = lo;
+        P.qs2[b] = hi;
+        P.d[b] = dd;
+    }
+}
+
+// IQ4_NL (18 B / 32) -> Q8_0 planes (kquants.go:7-27 then quantizeQ8Rows).
+__constant__ int8_t kIQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+__global__ void pack_iq4nl_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *p = raw + b * 18;
+        const double d = f16_to_f64(ld16(p));
+        double v[32];
+        for (int j = 0; j < 16; j++) {
+            v[j] = d * (double)kIQ4NL[p[2 + j] & 0x0f];
+            v[j + 16] = d * (double)kIQ4NL[p[2 + j] >> 4];
+        }
+        int4 lo, hi;
+        uint16_t dd;
+        q8_from_f64(v, lo, hi, dd);
+        P.qs[b] = lo;
+        P.qs2[b] = hi;
+        P.d[b] = dd;
+    }
+}
+
+// fp32 rows -> Q8_0 planes (quantizeQ8RowsF32, gguf.go:1143-1176).
+__global__ void pack_f32_kernel(const float *__restrict__ w, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const float *v = w + b * 32;
+        float maxAbs = 0.0f;
+        for (int i = 0; i < 32; i++) {
+            float a = __builtin_fabsf(v[i]);
+            if (a > maxAbs) maxAbs = a;
+        }
+        float scale = 0.0f;
+        if (maxAbs > 0) scale = maxAbs / 127.0f;
+        P.d[b] = f64_to_f16_trunc((double)scale);
+        const float inv = 1.0f / scale;
+        uint32_t q[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int i = 0; i < 32; i++) {
+            double val = (double)(v[i] * inv);
+            if (val > 127) val = 127;
+            else if (val < -128) val = -128;
+            q[i >> 2] |= f64_to_i8_byte(round(val)) << (8 * (i & 3));
+        }
+        P.qs[b] = make_int4((int)q[0], (int)q[1], (int)q[2], (int)q[3]);
+        P.qs2[b] = make_int4((int)q[4], (int)q[5], (int)q[6], (int)q[7]);
+    }
+}
+
+inline int grid_for(int64_t nb) {
+    int64_t g = (nb + 255) / 256;
+    return g > 65536 ? 65536 : (int)(g < 1 ? 1 : g);
+}
+
+}  // namespace
+
+sllm_status pack_from_raw(int fmt, const uint8_t *raw_dev, int rows, int G, const MutPlanes &P, int *err_dev,
+                          hipStream_t s) {
+    const int64_t nb = (int64_t)rows * G;
+    hipLaunchKernelGGL(pack_raw_kernel, dim3(grid_for(nb)), dim3(256), 0, s, fmt, raw_dev, nb, P, err_dev);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+sllm_status pack_from_gguf(uint32_t t, const uint8_t *raw_dev, int rows, int cols, const MutPlanes &P,
+                           hipStream_t s) {
+    const int64_t nb = (int64_t)rows * (cols / 32);
+    switch (t) {
+    case 12: hipLaunchKernelGGL(pack_q4k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    case 13: hipLaunchKernelGGL(pack_q5k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    case 14: hipLaunchKernelGGL(pack_q6k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    case 20: hipLaunchKernelGGL(pack_iq4nl_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    default: return set_error(SLLM_ERR_QTYPE, "pack_from_gguf: not a remapped type");
+    }
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s) {
+    const int64_t nb = (int64_t)rows * (cols / 32);
+    hipLaunchKernelGGL(pack_f32_kernel, dim3(grid_for(nb)), dim3(256), 0, s, w_dev, nb, P);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+}  // namespace sllm

@@ -1,0 +1,258 @@
+"""Python host side of the MI355X quantized-matmul path (ctypes over libsllm_qmm.so).
+
+Mirrors the reference's Go interface for this path so callers and tests read
+like the reference's own:
+
+=============================================  =======================================
+reference (scriptling-llm-lib)                 here
+=============================================  =======================================
+``QuantWeight`` (gguf.go:73-79)                :class:`QuantWeight` (host Raw) and
+                                               :class:`DeviceWeight` (HBM planes)
+``loadWeightF32Direct`` (gguf.go:818-934)      :func:`load_weight_f32_direct`
+``quantizeQ8RowsF32`` (gguf.go:1136-1186)      :func:`quantize_q8_rows_f32`
+``modelMatmulQuantIntoF32`` (float32_ops.go:379)  :func:`model_matmul_quant_into_f32`
+``modelMatmulRowQuantIntoF32`` (:620)          :func:`model_matmul_row_quant_into_f32`
+``argmaxF32`` (float32_ops.go:812)             :func:`argmax_f32_dev`
+=============================================  =======================================
+
+There is no CPU fallback: if the shared library or the GPU is missing every
+call raises :class:`SllmError`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from dataclasses import dataclass
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PKG_ROOT = os.path.dirname(HERE)
+REPO_ROOT = os.path.dirname(PKG_ROOT)
+LIB_PATH = os.path.join(PKG_ROOT, "libsllm_qmm.so")
+HEADER_PATH = os.path.join(REPO_ROOT, "include", "sllm_qmm.h")
+
+QTYPES = {"q8": 0, "q4": 1, "q4_1": 2, "q5": 3, "q5k1": 4}
+QTYPE_NAMES = {v: k for k, v in QTYPES.items()}
+RAW_BLOCK_BYTES = {"q8": 34, "q4": 18, "q4_1": 20, "q5": 22, "q5k1": 40}
+# Bytes the device planes hold (and a GEMV streams) per 32-element block.
+PLANE_BLOCK_BYTES = {"q8": 34, "q4": 18, "q4_1": 20, "q5": 22, "q5k1": 26}
+
+STATUS = {0: "SLLM_OK", 1: "SLLM_ERR_ARG", 2: "SLLM_ERR_QTYPE", 3: "SLLM_ERR_SHAPE",
+          4: "SLLM_ERR_DEVICE", 5: "SLLM_ERR_OOM", 6: "SLLM_ERR_FORMAT"}
+
+
+class SllmError(RuntimeError):
+    def __init__(self, status: int, msg: str):
+        super().__init__(f"{STATUS.get(status, status)}: {msg}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libsllm_qmm.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise SllmError(4, f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    P, i32, sz = C.c_void_p, C.c_int, C.c_size_t
+    W = C.c_void_p
+    L.sllm_weight_from_quant.argtypes = [C.c_char_p, P, sz, i32, i32, i32, C.POINTER(W)]
+    L.sllm_weight_from_gguf.argtypes = [C.c_uint32, P, sz, i32, i32, C.POINTER(W)]
+    L.sllm_weight_from_f32.argtypes = [P, i32, i32, C.POINTER(W)]
+    L.sllm_weight_destroy.argtypes = [W]
+    L.sllm_weight_info.argtypes = [W, C.POINTER(i32), C.POINTER(i32), C.POINTER(i32), C.POINTER(i32),
+                                   C.POINTER(sz)]
+    L.sllm_weight_export.argtypes = [W, P, sz]
+    L.sllm_matmul_quant_into_f32.argtypes = [W, P, i32, i32, P]
+    L.sllm_matmul_row_quant_into_f32.argtypes = [W, P, P]
+    L.sllm_matmul_dev.argtypes = [W, P, i32, i32, P, P]
+    L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
+    L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
+    L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
+    L.sllm_set_param.argtypes = [C.c_char_p, i32]
+    for name in exported_names():  # raises AttributeError if a declared symbol is missing
+        f = getattr(L, name)
+        if name in ("sllm_last_error", "sllm_kernel_info"):
+            f.restype = C.c_char_p
+        elif name == "sllm_weight_destroy":
+            f.restype = None
+        else:
+            f.restype = i32
+    _lib = L
+    return L
+
+
+def exported_names() -> list[str]:
+    """Every function the public header declares."""
+    with open(HEADER_PATH) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(sllm_[a-z0-9_]+)\s*\(", text)))
+
+
+def _check(st: int) -> None:
+    if st != 0:
+        msg = lib().sllm_last_error()
+        raise SllmError(st, msg.decode() if msg else "")
+
+
+def _ptr(a: np.ndarray) -> int:
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("array must be C-contiguous")
+    return a.ctypes.data
+
+
+def init() -> None:
+    _check(lib().sllm_init())
+
+
+def kernel_info() -> str:
+    return lib().sllm_kernel_info().decode()
+
+
+def set_param(name: str, value: int) -> None:
+    _check(lib().sllm_set_param(name.encode(), int(value)))
+
+
+@dataclass
+class QuantWeight:
+    """The reference's QuantWeight (gguf.go:73-79): QType, Raw, Groups, Rows, Cols."""
+    qtype: str
+    raw: np.ndarray
+    groups: int
+    rows: int
+    cols: int
+
+
+class DeviceWeight:
+    """A weight repacked into HBM planes (opaque sllm_weight handle)."""
+
+    def __init__(self, handle: int):
+        self._h = C.c_void_p(handle)
+        q, g, r, c = C.c_int(), C.c_int(), C.c_int(), C.c_int()
+        n = C.c_size_t()
+        _check(lib().sllm_weight_info(self._h, C.byref(q), C.byref(g), C.byref(r), C.byref(c), C.byref(n)))
+        self.qtype = QTYPE_NAMES[q.value]
+        self.groups, self.rows, self.cols, self.raw_bytes = g.value, r.value, c.value, n.value
+
+    @property
+    def handle(self) -> C.c_void_p:
+        if self._h is None:
+            raise SllmError(1, "weight already destroyed")
+        return self._h
+
+    @property
+    def plane_bytes(self) -> int:
+        return self.rows * self.groups * PLANE_BLOCK_BYTES[self.qtype]
+
+    @classmethod
+    def from_quant(cls, w: QuantWeight) -> "DeviceWeight":
+        raw = np.ascontiguousarray(np.frombuffer(memoryview(w.raw).cast("B"), np.uint8))
+        h = C.c_void_p()
+        _check(lib().sllm_weight_from_quant(w.qtype.encode(), _ptr(raw), raw.nbytes, w.groups, w.rows, w.cols,
+                                            C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_gguf(cls, ggml_type: int, raw, rows: int, cols: int) -> "DeviceWeight":
+        raw = np.ascontiguousarray(np.frombuffer(memoryview(raw).cast("B"), np.uint8))
+        h = C.c_void_p()
+        _check(lib().sllm_weight_from_gguf(int(ggml_type), _ptr(raw), raw.nbytes, rows, cols, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_f32(cls, w: np.ndarray) -> "DeviceWeight":
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        rows, cols = w.shape
+        h = C.c_void_p()
+        _check(lib().sllm_weight_from_f32(_ptr(w), rows, cols, C.byref(h)))
+        return cls(h.value)
+
+    def export(self) -> np.ndarray:
+        """QuantWeight.Raw bytes rebuilt from the device planes."""
+        out = np.empty(self.raw_bytes, np.uint8)
+        _check(lib().sllm_weight_export(self.handle, _ptr(out), out.nbytes))
+        return out
+
+    def to_quant(self) -> QuantWeight:
+        return QuantWeight(self.qtype, self.export(), self.groups, self.rows, self.cols)
+
+    def close(self) -> None:
+        if self._h is not None:
+            lib().sllm_weight_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def load_weight_f32_direct(ggml_type: int, raw, rows: int, cols: int) -> DeviceWeight:
+    """gguf.go:818-934 for the int8-kernel types (8, 2, 3, 6, 12, 13, 14, 20)."""
+    return DeviceWeight.from_gguf(ggml_type, raw, rows, cols)
+
+
+def quantize_q8_rows_f32(flat: np.ndarray, rows: int, cols: int) -> DeviceWeight:
+    """gguf.go:1136-1186 on the GPU (the tied-head path, model_f32.go:150-152)."""
+    return DeviceWeight.from_f32(np.asarray(flat, np.float32).reshape(rows, cols))
+
+
+def model_matmul_quant_into_f32(w: DeviceWeight, x_data: np.ndarray, x_rows: int, x_cols: int,
+                                dst: np.ndarray | None = None):
+    """float32_ops.go:379-460: returns (dst, xRows, Rows) like the Go function."""
+    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    if x.size < x_rows * x_cols:
+        raise SllmError(1, "xData shorter than xRows*xCols")
+    n = x_rows * w.rows
+    if dst is None or dst.size < n or dst.dtype != np.float32 or not dst.flags["C_CONTIGUOUS"]:
+        dst = np.empty(n, np.float32)  # growSlice (float32_ops.go:79-84)
+    _check(lib().sllm_matmul_quant_into_f32(w.handle, _ptr(x), x_rows, x_cols, _ptr(dst)))
+    return dst[:n], x_rows, w.rows
+
+
+def model_matmul_row_quant_into_f32(w: DeviceWeight, normed: np.ndarray, dst: np.ndarray | None = None):
+    """float32_ops.go:620-707: one activation row."""
+    x = np.ascontiguousarray(normed, dtype=np.float32).reshape(-1)
+    if dst is None or dst.size < w.rows:
+        dst = np.empty(w.rows, np.float32)
+    _check(lib().sllm_matmul_row_quant_into_f32(w.handle, _ptr(x), _ptr(dst)))
+    return dst[: w.rows]
+
+
+def matmul_dev(w: DeviceWeight, x_ptr: int, x_rows: int, x_cols: int, dst_ptr: int, stream: int = 0) -> None:
+    """Device-resident matmul: raw device pointers, enqueued on `stream`."""
+    _check(lib().sllm_matmul_dev(w.handle, C.c_void_p(x_ptr), x_rows, x_cols, C.c_void_p(dst_ptr),
+                                 C.c_void_p(stream)))
+
+
+def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:
+    out = C.c_int()
+    _check(lib().sllm_argmax_dev(C.c_void_p(v_ptr), n, C.byref(out), C.c_void_p(stream)))
+    return out.value
+
+
+def debug_quantize_act(x: np.ndarray):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    rows = x.size // K
+    xq = np.empty(x.shape, np.int8)
+    xs = np.empty(x.shape[:-1] + (K // 32,), np.float32)
+    sx = np.empty(x.shape[:-1] + (K // 32,), np.int32)
+    _check(lib().sllm_debug_quantize_act(_ptr(x), rows, K, _ptr(xq), _ptr(xs), _ptr(sx)))
+    return xq, xs, sx
+
+
+def debug_block_dots(w: DeviceWeight, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, w.cols)
+    M = x.shape[0]
+    shape = (M, w.rows, w.groups, 2) if w.qtype == "q5k1" else (M, w.rows, w.groups)
+    out = np.empty(shape, np.int32)
+    _check(lib().sllm_debug_block_dots(w.handle, _ptr(x), M, w.cols, _ptr(out)))
+    return out
