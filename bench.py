@@ -1,0 +1,259 @@
+"""Benchmark of the MI355X quantized-matmul path (one JSON line on stdout).
+
+Workload (the one the metric is quoted on): one Llama-3-8B
+layer's decode GEMVs at M = 1 token -
+    gate, up : Q4_K 14336 x 4096, remapped at load to Q4_1 (20 B / 32 weights)
+    down     : Q6_K 4096 x 14336, requantized at load to Q8_0 (34 B / 32)
+A step is the three GEMVs over one layer's weights; steps rotate over enough
+layer copies (> 1 GiB) that no step finds its weights in the 256 MB MALL.
+Inputs are synthetic, already resident in HBM; the remap runs once at load.
+
+value        = algorithmic bytes per step x steps / elapsed   (GB/s, whole job)
+roofline     = dominant kernel (the Q8_0 down GEMV): algorithmic bytes per launch
+               / its mean duration, timed with HIP events around each launch
+cpu_baseline = the reference's CPU kernels restated with AVX2/AVX-VNNI intrinsics
+               and its worker pool (oracle/refcpu_simd.c), on a bounded sample
+extra        = decode tok/s over all 225 GEMVs of a 32-layer Q4_K_M 8B-shaped
+               model + Q6_K head (weights only; attention etc. not included)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "scriptling-llm-lib_amd"))
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "quant GEMV GB/s (% of 8 TB/s HBM); Q4_K_M 8B-shape decode tok/s"
+
+
+def algo_bytes(w, m_rows: int = 1) -> int:
+    """Weight plane bytes + fp32 activations in + fp32 outputs out."""
+    return w.plane_bytes + 4 * w.cols * m_rows + 4 * w.rows * m_rows
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=8, help="layer copies rotated over (>1 GiB)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--decode-tokens", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "Each GPU would own a slice of the weight rows; see the sharding note in DESIGN.md.",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import sllm_qmm as sq
+    from sllm_qmm import synth
+
+    torch.cuda.set_device(0)
+    sq.init()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+
+    H, F = 4096, 14336
+    print(f"[bench] building {args.layers} layer copies of C3 weights", file=sys.stderr, flush=True)
+    gate_raw = synth.q4k_blocks(100, F, H)
+    up_raw = synth.q4k_blocks(101, F, H)
+    down_raw = synth.q6k_blocks(102, H, F)
+    layers = []
+    for _ in range(args.layers):
+        layers.append((sq.load_weight_f32_direct(synth.GGML_Q4_K, gate_raw, F, H),
+                       sq.load_weight_f32_direct(synth.GGML_Q4_K, up_raw, F, H),
+                       sq.load_weight_f32_direct(synth.GGML_Q6_K, down_raw, H, F)))
+    g0, u0, d0 = layers[0]
+    x = torch.from_numpy(synth.normal(1, H)).cuda()
+    h = torch.from_numpy(synth.normal(2, F)).cuda()
+    yg = torch.empty(F, device="cuda")
+    yu = torch.empty(F, device="cuda")
+    yd = torch.empty(H, device="cuda")
+    step_bytes = algo_bytes(g0) + algo_bytes(u0) + algo_bytes(d0)
+
+    def step(i, ev=None):
+        g, u, d = layers[i % len(layers)]
+        sq.matmul_dev(g, x.data_ptr(), 1, H, yg.data_ptr(), sp)
+        sq.matmul_dev(u, x.data_ptr(), 1, H, yu.data_ptr(), sp)
+        if ev is not None:
+            ev[0].record(stream)
+        sq.matmul_dev(d, h.data_ptr(), 1, F, yd.data_ptr(), sp)
+        if ev is not None:
+            ev[1].record(stream)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    elapsed_ms = t0.elapsed_time(t1)
+    ms_per_step = elapsed_ms / args.steps
+    value = step_bytes * args.steps / (elapsed_ms * 1e-3) / 1e9
+
+    # Dominant kernel: the Q8_0 down GEMV (46% of the step's bytes), events around each launch.
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    for i in range(args.steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    down_us = float(np.mean([a.elapsed_time(b) for a, b in evs])) * 1e3
+    down_bytes = algo_bytes(d0)
+    achieved = down_bytes / (down_us * 1e-6) / 1e9
+
+    # Same for the Q4_1 gate GEMV (reported in extra).
+    def time_one(widx, xin, yout, n):
+        evl = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for i in range(n):
+            w = layers[i % len(layers)][widx]
+            evl[i][0].record(stream)
+            sq.matmul_dev(w, xin.data_ptr(), 1, w.cols, yout.data_ptr(), sp)
+            evl[i][1].record(stream)
+        torch.cuda.synchronize()
+        return float(np.mean([a.elapsed_time(b) for a, b in evl])) * 1e3
+
+    gate_us = time_one(0, x, yg, args.steps)
+
+    extra = {
+        "gate_q4_1_gemv_us": round(gate_us, 3),
+        "gate_q4_1_gemv_GBps": round(algo_bytes(g0) / (gate_us * 1e-6) / 1e9, 1),
+        "down_q8_0_gemv_us": round(down_us, 3),
+        "kernel_info": sq.kernel_info(),
+    }
+
+    if not args.no_decode:
+        extra.update(decode_tok_s(sq, synth, torch, stream, args.decode_tokens))
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(layers[0], step_bytes)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3: Llama-3-8B Q4_K_M layer decode GEMVs, M=1: Q4_K gate+up 14336x4096 -> Q4_1, "
+                        "Q6_K down 4096x14336 -> Q8_0",
+            "bytes_per_step": step_bytes,
+            "rotating_layer_copies": args.layers,
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "gemv_kernel<Q8_0> (Q6_K->Q8_0 down 4096x14336)",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
+    """All linears of one decode token of a 32-layer Q4_K_M Llama-3-8B shape + Q6_K head."""
+    import numpy as np
+    H, F, KV, V, L = 4096, 14336, 1024, 128256, 32
+    print("[bench] building the 32-layer decode weight set", file=sys.stderr, flush=True)
+    q4k_hh = synth.q4k_blocks(200, H, H)
+    q4k_kv = synth.q4k_blocks(201, KV, H)
+    q4k_fh = synth.q4k_blocks(202, F, H)
+    q6k_hf = synth.q6k_blocks(203, H, F)
+    q6k_head = synth.q6k_blocks(204, V, H)
+    mk = sq.load_weight_f32_direct
+    layer_ws = []
+    for _ in range(L):
+        layer_ws.append([mk(12, q4k_hh, H, H), mk(12, q4k_kv, KV, H), mk(12, q4k_kv, KV, H),
+                         mk(12, q4k_hh, H, H), mk(12, q4k_fh, F, H), mk(12, q4k_fh, F, H),
+                         mk(14, q6k_hf, H, F)])
+    head = mk(14, q6k_head, V, H)
+    tok_bytes = sum(w.plane_bytes for ws in layer_ws for w in ws) + head.plane_bytes
+    xh = torch.from_numpy(synth.normal(3, H)).cuda()
+    xf = torch.from_numpy(synth.normal(4, F)).cuda()
+    out = torch.empty(V, device="cuda")
+    sp = stream.cuda_stream
+
+    def token():
+        for ws in layer_ws:
+            for w in ws:
+                src = xf if w.cols == F else xh
+                sq.matmul_dev(w, src.data_ptr(), 1, w.cols, out.data_ptr(), sp)
+        sq.matmul_dev(head, xh.data_ptr(), 1, H, out.data_ptr(), sp)
+
+    for _ in range(3):
+        token()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(tokens):
+        token()
+    b.record(stream)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / tokens
+    del layer_ws, head
+    return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
+            "decode_weight_bytes_per_token": tok_bytes,
+            "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
+            "decode_note": "225 GEMV launches per token (32 layers x 7 + head); attention, norms not included"}
+
+
+def cpu_baseline(layer, step_bytes: int) -> dict:
+    """Restated reference CPU path (AVX2/AVX-VNNI, parallel.go pool) on one C3 step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle  # the cpu_baseline leg is the one bench.py part allowed to use oracle/
+    from sllm_qmm import synth
+
+    B = oracle.baseline()
+    workers = B.bl_workers()
+    g, u, d = layer
+    gr, ur, dr = g.export(), u.export(), d.export()
+    x = synth.normal(1, g.cols).reshape(1, -1)
+    hx = synth.normal(2, d.cols).reshape(1, -1)
+    t0 = time.time()
+    tg = oracle.baseline_time("q4_1", gr, g.rows, x, reps=3, trials=5)
+    tu = oracle.baseline_time("q4_1", ur, u.rows, x, reps=3, trials=5)
+    td = oracle.baseline_time("q8", dr, d.rows, hx, reps=3, trials=5)
+    wall = time.time() - t0
+    sec = tg + tu + td
+    return {
+        "value": round(step_bytes / sec / 1e9, 2),
+        "unit": "GB/s",
+        "cores": workers,
+        "kind": "port",
+        "sample": f"one C3 step (gate+up Q4_1 VNNI/AVX2, down Q8_0 VNNI/AVX2), min of 5 trials x 3 reps each; "
+                  f"{sec * 1e3:.2f} ms/step, {wall:.1f} s wall; vnni={bool(B.bl_has_vnni())}",
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -74,6 +74,8 @@ def lib() -> C.CDLL:
         L.ref_q5_row.argtypes = [P, P, i32]
         L.ref_matmul_quant.argtypes = [C.c_char_p, P, i32, i32, P, i32, P]
         L.ref_argmax.argtypes = [P, i32]
+        L.ref_scale_min_k4.argtypes = [i32, P, P, P]
+        L.ref_block_bytes.argtypes = [C.c_char_p]
         _lib = L
     return _lib
 
@@ -214,3 +216,50 @@ def row_q41q8(w, xq, xs, sxq):
 
 def row_q5(w, x):
     return lib().ref_q5_row(_p(w), _p(x), x.size // 32)
+
+
+def scale_min_k4(j: int, q: np.ndarray):
+    q = np.ascontiguousarray(q, dtype=np.uint8)
+    sc, m = C.c_uint8(), C.c_uint8()
+    lib().ref_scale_min_k4(j, _p(q), C.addressof(sc), C.addressof(m))
+    return sc.value, m.value
+
+
+_bl = None
+
+
+def baseline() -> C.CDLL:
+    """The threaded AVX2/AVX-VNNI restatement (refcpu_simd.c): the cpu_baseline leg."""
+    global _bl
+    if _bl is None:
+        if not os.path.exists(BASELINE_PATH):
+            raise RuntimeError(f"baseline not built: {BASELINE_PATH} missing")
+        B = C.CDLL(BASELINE_PATH)
+        B.bl_matmul.argtypes = [C.c_char_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p]
+        B.bl_time_matmul.argtypes = [C.c_char_p, C.c_void_p, C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_void_p,
+                                     C.c_int, C.c_int]
+        B.bl_time_matmul.restype = C.c_double
+        B.bl_set_workers.argtypes = [C.c_int]
+        _bl = B
+    return _bl
+
+
+def baseline_matmul(qtype: str, raw: np.ndarray, N: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    M = x.size // K
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    dst = np.empty((M, N), np.float32)
+    if baseline().bl_matmul(qtype.encode(), _p(raw), N, K, _p(x), M, _p(dst)):
+        raise ValueError(qtype)
+    return dst
+
+
+def baseline_time(qtype: str, raw: np.ndarray, N: int, x: np.ndarray, reps: int, trials: int = 7) -> float:
+    """Seconds per matmul: min over `trials` of the mean of `reps` calls (q8q8.go:280-294)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    M = x.size // K
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    dst = np.empty((M, N), np.float32)
+    return baseline().bl_time_matmul(qtype.encode(), _p(raw), N, K, _p(x), M, _p(dst), reps, trials)

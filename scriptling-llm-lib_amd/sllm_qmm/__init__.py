@@ -59,6 +59,13 @@ def lib() -> C.CDLL:
         return _lib
     if not os.path.exists(LIB_PATH):
         raise SllmError(4, f"{LIB_PATH} is missing: build it with __graft_entry__.build()")
+    # One HIP runtime per process: torch ships its own libamdhip64.so.7. Loading
+    # torch first makes the library bind to that same runtime (same SONAME)
+    # instead of bringing up a second one from /opt/rocm next to it.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     L = C.CDLL(LIB_PATH)
     P, i32, sz = C.c_void_p, C.c_int, C.c_size_t
     W = C.c_void_p
