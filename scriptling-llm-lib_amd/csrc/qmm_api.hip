@@ -214,9 +214,9 @@ const char *sllm_kernel_info(void) {
     const Tuning &t = tuning();
     char buf[512];
     std::snprintf(buf, sizeof buf,
-                  "sllm_qmm gfx950 planes-v1 | gemv: %d waves/WG, grid cap %d, K-split to >=%d batches, "
-                  "fused Q8_0 LDS prologue | gemm: int8 MFMA from xRows>=%d",
-                  t.gemv_waves, t.gemv_grid_cap, t.gemv_min_batches, t.gemm_min_rows);
+                  "sllm_qmm gfx950 planes-v1 | gemv: persistent, <=%d waves/WG, %d WG/CU, fused Q8_0 LDS "
+                  "prologue, non-temporal weight stream | gemm: int8 MFMA from xRows>=%d",
+                  t.gemv_waves, t.gemv_wg_per_cu, t.gemm_min_rows);
     info = buf;
     return info.c_str();
 }
@@ -224,9 +224,10 @@ const char *sllm_kernel_info(void) {
 sllm_status sllm_set_param(const char *name, int value) {
     if (!name) return set_error(SLLM_ERR_ARG, "null name");
     Tuning &t = tuning();
-    if (!std::strcmp(name, "gemv_grid_cap") && value >= 1) t.gemv_grid_cap = value;
-    else if (!std::strcmp(name, "gemv_waves") && (value == 4 || value == 8 || value == 16)) t.gemv_waves = value;
-    else if (!std::strcmp(name, "gemv_min_batches") && value >= 1) t.gemv_min_batches = value;
+    if (!std::strcmp(name, "gemv_waves") && (value == 4 || value == 8 || value == 16)) t.gemv_waves = value;
+    else if (!std::strcmp(name, "gemv_wg_per_cu") && value >= 1 && value <= 8) t.gemv_wg_per_cu = value;
+    else if (!std::strcmp(name, "gemv_max_nb") && value >= 1 && value <= 8) t.gemv_max_nb = value;
+    else if (!std::strcmp(name, "gemv_inflight_kb") && value >= 64) t.gemv_inflight_kb = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;

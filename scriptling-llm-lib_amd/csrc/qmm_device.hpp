@@ -55,37 +55,64 @@ __device__ __forceinline__ int quant_trunc_clamp(float p) {
     return q;
 }
 
-// One quarter of a 32-element block (4 consecutive fp32 values held by one of
-// the 8 lanes that share the block; the 8 lanes are consecutive and aligned).
-// Returns the 4 int8 codes packed little-endian; *scale and *sum receive the
-// block's fp32 scale and Σq in every lane of the 8. q8q8.go:96-125.
-__device__ __forceinline__ uint32_t quantize_quarter(float4 v, float *scale, int *sum) {
-    float a = 0.0f, t;
-    t = __builtin_fabsf(v.x); a = t > a ? t : a;
-    t = __builtin_fabsf(v.y); a = t > a ? t : a;
-    t = __builtin_fabsf(v.z); a = t > a ? t : a;
-    t = __builtin_fabsf(v.w); a = t > a ? t : a;
+// Combine a value across the TPB consecutive, aligned lanes that share a block
+// (TPB = 1, 2, 4 or 8) with DPP moves; every lane of the group receives it.
+template <int CTRL>
+__device__ __forceinline__ int dpp_mov(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+template <int TPB>
+__device__ __forceinline__ float group_max(float a) {
+    // max of non-NaN magnitudes (a is never NaN here): order-independent
+    float o;
+    if (TPB >= 2) { o = __builtin_bit_cast(float, dpp_mov<0xb1>(__builtin_bit_cast(int, a))); a = o > a ? o : a; }
+    if (TPB >= 4) { o = __builtin_bit_cast(float, dpp_mov<0x4e>(__builtin_bit_cast(int, a))); a = o > a ? o : a; }
+    if (TPB >= 8) { o = __builtin_bit_cast(float, dpp_mov<0x141>(__builtin_bit_cast(int, a))); a = o > a ? o : a; }
+    return a;
+}
+template <int TPB>
+__device__ __forceinline__ int group_sum(int v) {
+    if (TPB >= 2) v += dpp_mov<0xb1>(v);   // lane ^ 1
+    if (TPB >= 4) v += dpp_mov<0x4e>(v);   // lane ^ 2
+    if (TPB >= 8) v += dpp_mov<0x141>(v);  // other quad of the 8
+    return v;
+}
+
+// quantizeActivationsQ8 (q8q8.go:96-125) for one 32-element block spread over
+// TPB lanes, each holding 8/TPB float4 (elements 32/TPB * sub ...). Every lane
+// returns its 8/TPB packed code words; scale and Σq are the block's. maxAbs
+// over |x| (NaN never wins the `>` compare), scale = maxAbs/127 and inv =
+// 1/scale in IEEE fp32 (0 for an all-zero block), q = clamp(int32(x*inv)).
+// The maximum and the integer sum do not depend on how the lanes combine.
+template <int TPB>
+__device__ __forceinline__ void quantize_part(const float4 *v, int *w, float &scale, int &sum) {
+    float a = 0.0f;
 #pragma unroll
-    for (int off = 1; off < 8; off <<= 1) {
-        float o = __shfl_xor(a, off);
-        a = o > a ? o : a;
+    for (int k = 0; k < 8 / TPB; k++) {
+        float t;
+        t = __builtin_fabsf(v[k].x); a = t > a ? t : a;
+        t = __builtin_fabsf(v[k].y); a = t > a ? t : a;
+        t = __builtin_fabsf(v[k].z); a = t > a ? t : a;
+        t = __builtin_fabsf(v[k].w); a = t > a ? t : a;
     }
+    a = group_max<TPB>(a);
     float s = 0.0f, inv = 0.0f;
     if (a > 0.0f) {
         s = a / 127.0f;
         inv = 1.0f / s;
     }
-    int q0 = quant_trunc_clamp(v.x * inv);
-    int q1 = quant_trunc_clamp(v.y * inv);
-    int q2 = quant_trunc_clamp(v.z * inv);
-    int q3 = quant_trunc_clamp(v.w * inv);
-    int sm = q0 + q1 + q2 + q3;
+    int sm = 0;
 #pragma unroll
-    for (int off = 1; off < 8; off <<= 1) sm += __shfl_xor(sm, off);
-    *scale = s;
-    *sum = sm;
-    return (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-           ((uint32_t)(q3 & 0xff) << 24);
+    for (int k = 0; k < 8 / TPB; k++) {
+        const int q0 = quant_trunc_clamp(v[k].x * inv);
+        const int q1 = quant_trunc_clamp(v[k].y * inv);
+        const int q2 = quant_trunc_clamp(v[k].z * inv);
+        const int q3 = quant_trunc_clamp(v[k].w * inv);
+        w[k] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (int)((uint32_t)(q3 & 0xff) << 24);
+        sm = __builtin_amdgcn_sdot4(w[k], 0x01010101, sm, false);
+    }
+    scale = s;
+    sum = group_sum<TPB>(sm);
 }
 
 // ---------------------------------------------------------- block dots ----

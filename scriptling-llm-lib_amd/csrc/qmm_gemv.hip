@@ -1,19 +1,20 @@
 // Decode GEMV (xRows < 64) for every weight format.
 //
-// One launch computes dst[m][n] = Σ_g term(m, n, g) for up to MT activation rows:
-//   prologue  every workgroup quantizes the activation rows into LDS with the
-//             bit-exact Q8_0 quantizer (or, for Q5_0, stages the fp32 rows);
-//   main      rows are taken in batches of R = waves / S rows per workgroup; the
-//             S waves of a row each own a contiguous slice of its blocks, and
-//             lane l of a wave owns blocks slice_start + l + 64 i. A lane loads
-//             its blocks' planes with 16-byte loads (consecutive lanes read
-//             consecutive 16 B), forms the reference's per-block term exactly,
-//             and accumulates; the wave then reduces across lanes and the S
-//             slice partials are added in slice order (fixed order, so results
-//             are bit-reproducible run to run).
+// Persistent launch (at most gemv_wg_per_cu workgroups per CU). Each wave owns
+// rows wv, wv + TW, ... and streams them as units of NB blocks per lane (one
+// K-chunk of a row), keeping D units in flight in a register ring.
+//   1. threads that own an activation block issue its loads first, then every
+//      wave issues its first D units of weight loads, then the owners quantize
+//      their block into LDS with the bit-exact Q8_0 quantizer (Q5_0: stage the
+//      fp32 block) - the weight stream is in flight during the prologue;
+//   2. main loop: lane l owns blocks l + 64 i of each K-chunk; it reads the
+//      block's activation codes from LDS, forms the reference's per-block term
+//      exactly and accumulates; at a row's end the wave reduces across lanes
+//      (fixed order) and parks the sum in lane (row ordinal); results are
+//      stored once at the end, one coalesced store per wave.
 // The per-block term equals the reference's bit for bit; only the order in
-// which the terms of a row are added differs from the reference's sequential
-// loop (reassociation).
+// which a row's terms are added differs from the reference's sequential loop
+// (reassociation), and that order is fixed, so results are reproducible.
 #include <hip/hip_runtime.h>
 
 #include "qmm_device.hpp"
@@ -23,59 +24,69 @@ namespace sllm {
 
 namespace {
 
-constexpr int kMaxWaves = 16;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Weight planes are read once per GEMV: non-temporal loads keep them from
+// displacing the activations and other reused data in L2 / MALL.
+__device__ __forceinline__ int4 ld_nt(const int4 *p) {
+    const v4i t = __builtin_nontemporal_load((const v4i *)p);
+    return make_int4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint16_t ld_nt(const uint16_t *p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ uint32_t ld_nt(const uint32_t *p) { return __builtin_nontemporal_load(p); }
 
 // LDS image of the prologue for MT activation rows of G blocks.
 struct ActView {
-    int4 *xl;    // [MT][G] elements 0..15 of each block (int8)
-    int4 *xh;    // [MT][G] elements 16..31
-    float *xs;   // [MT][G] activation scale
-    int *sx;     // [MT][G] Σxq
-    float *xf;   // Q5_0: [MT][G][kXfStride] fp32 activations
-    float *red;  // [kMaxWaves][2*MT] slice partials
+    int4 *xl;   // [MT][G] elements 0..15 of each block (int8)
+    int4 *xh;   // [MT][G] elements 16..31
+    float *xs;  // [MT][G] activation scale
+    int *sx;    // [MT][G] Σxq
+    float *xf;  // Q5_0: [MT][G][kXfStride] fp32 activations
 };
 
 __host__ __device__ inline size_t act_lds_bytes(int fmt, int MT, int G) {
-    size_t red = (size_t)kMaxWaves * 2 * MT * sizeof(float);
-    if (fmt == SLLM_Q5_0) return (size_t)MT * G * kXfStride * sizeof(float) + red;
-    return (size_t)MT * G * (2 * sizeof(int4) + sizeof(float) + sizeof(int)) + red;
+    if (fmt == SLLM_Q5_0) return (size_t)MT * G * kXfStride * sizeof(float);
+    return (size_t)MT * G * (2 * sizeof(int4) + sizeof(float) + sizeof(int));
 }
 
 __device__ inline ActView carve_act(unsigned char *lds, int fmt, int MT, int G) {
     ActView v{};
     if (fmt == SLLM_Q5_0) {
         v.xf = (float *)lds;
-        v.red = v.xf + (size_t)MT * G * kXfStride;
     } else {
         v.xl = (int4 *)lds;
         v.xh = v.xl + (size_t)MT * G;
         v.xs = (float *)(v.xh + (size_t)MT * G);
         v.sx = (int *)(v.xs + (size_t)MT * G);
-        v.red = (float *)(v.sx + (size_t)MT * G);
     }
     return v;
 }
 
-// Prologue: quantize (or stage) M activation rows of K = 32 G fp32 into LDS.
-template <int FMT>
-__device__ inline void stage_activations(const float *__restrict__ x, int M, int G, const ActView &A) {
-    const int T = blockDim.x;
-    const int total = M * G * 8;  // 8 lanes per block, 4 elements each
-    for (int i = threadIdx.x; i < total; i += T) {
-        const int blk = i >> 3, sub = i & 7;
-        const float4 v = *(const float4 *)(x + (size_t)blk * 32 + sub * 4);
-        if (FMT == SLLM_Q5_0) {
-            *(float4 *)(A.xf + (size_t)blk * kXfStride + sub * 4) = v;
-        } else {
-            float s;
-            int sm;
-            uint32_t packed = quantize_quarter(v, &s, &sm);
-            int *dstw = (int *)((sub < 4) ? (A.xl + blk) : (A.xh + blk));
-            dstw[sub & 3] = (int)packed;
-            if (sub == 0) {
-                A.xs[blk] = s;
-                A.sx[blk] = sm;
-            }
+// Writes one lane's part (8/TPB float4 = 32/TPB elements) of activation block
+// blk into LDS: quantized codes + scale + Σq, or (Q5_0) the fp32 values.
+template <int FMT, int TPB>
+__device__ __forceinline__ void stage_part(const float4 *v, int blk, int sub, const ActView &A) {
+    constexpr int NV = 8 / TPB;
+    if (FMT == SLLM_Q5_0) {
+        float4 *d = (float4 *)(A.xf + (size_t)blk * kXfStride) + sub * NV;
+#pragma unroll
+        for (int k = 0; k < NV; k++) d[k] = v[k];
+    } else {
+        int w[NV];
+        float s;
+        int sm;
+        quantize_part<TPB>(v, w, s, sm);
+        // word j of the block (j = sub*NV + k): words 0..3 -> xl, 4..7 -> xh
+        int *lo = (int *)(A.xl + blk), *hi = (int *)(A.xh + blk);
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const int j = sub * NV + k;
+            if (j < 4) lo[j] = w[k];
+            else hi[j - 4] = w[k];
+        }
+        if (sub == 0) {
+            A.xs[blk] = s;
+            A.sx[blk] = sm;
         }
     }
 }
@@ -87,224 +98,391 @@ struct BlockRegs {
     uint32_t qh;
 };
 
-template <int FMT>
-__device__ __forceinline__ void load_block(const Planes &P, size_t idx, BlockRegs &b) {
-    b.q = P.qs[idx];
-    b.d = P.d[idx];
-    if (FMT == SLLM_Q8_0) b.q2 = P.qs2[idx];
-    if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) b.m = P.m[idx];
-    if (FMT == SLLM_Q5K1) b.dh = P.dh[idx];
-    if (FMT == SLLM_Q5_0 || FMT == SLLM_Q5K1) b.qh = P.qh[idx];
+template <class T>
+__device__ __forceinline__ const T *at(const T *base, uint32_t idx) {
+    // base + 32-bit byte offset: lets the loads use the SGPR-base + VGPR-offset form
+    return (const T *)((const char *)base + (uint64_t)(idx * (uint32_t)sizeof(T)));
 }
 
-// Adds block g's term for activation row m to acc (acc2: the Q5K1 high half).
 template <int FMT>
-__device__ __forceinline__ void block_term(const BlockRegs &b, const ActView &A, int G, int m, int g,
-                                           float &acc, float &acc2) {
-    const size_t a = (size_t)m * G + g;
+__device__ __forceinline__ void load_block(const Planes &P, uint32_t idx, BlockRegs &b) {
+    b.q = ld_nt(at(P.qs, idx));
+    b.d = ld_nt(at(P.d, idx));
+    if (FMT == SLLM_Q8_0) b.q2 = ld_nt(at(P.qs2, idx));
+    if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) b.m = ld_nt(at(P.m, idx));
+    if (FMT == SLLM_Q5K1) b.dh = ld_nt(at(P.dh, idx));
+    if (FMT == SLLM_Q5_0 || FMT == SLLM_Q5K1) b.qh = ld_nt(at(P.qh, idx));
+}
+
+// Blocks lane + 64 i (i < NB) of one unit, starting at plane index `base`.
+template <int FMT, int NB>
+__device__ __forceinline__ void load_unit(const Planes &P, BlockRegs (&u)[NB], uint32_t base) {
+#pragma unroll
+    for (int i = 0; i < NB; i++) load_block<FMT>(P, base + 64u * i, u[i]);
+}
+
+// Activation operands of one block, read from LDS.
+struct ActRegs {
+    int4 xl, xh;
+    float xs;
+    int sx;
+    float4 xf[8];
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_act(const ActView &A, size_t a, ActRegs &r) {
     if (FMT == SLLM_Q5_0) {
-        const float4 *xb = (const float4 *)(A.xf + a * kXfStride);
-        float sum = q5_block_sum(b.q, b.qh, xb);
-        float s = f16_lut(b.d);
-        float grp = s * sum;  // float32_ops.go:366 `s * sum`
-        acc = acc + grp;
-        return;
+        const float4 *src = (const float4 *)(A.xf + a * kXfStride);
+#pragma unroll
+        for (int k = 0; k < 8; k++) r.xf[k] = src[k];
+    } else {
+        r.xl = A.xl[a];
+        r.xh = A.xh[a];
+        r.xs = A.xs[a];
+        r.sx = A.sx[a];
     }
-    const int4 xl = A.xl[a], xh = A.xh[a];
-    const float xs = A.xs[a];
-    if (FMT == SLLM_Q8_0) {
+}
+
+// Adds one block's term to acc (acc2: the Q5K1 high half), in the reference's
+// operation order for that format.
+template <int FMT>
+__device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x, float &acc, float &acc2) {
+    if (FMT == SLLM_Q5_0) {
+        const float sum = q5_block_sum(b.q, b.qh, x.xf);
+        const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`
+        acc = acc + grp;
+    } else if (FMT == SLLM_Q8_0) {
         // q8q8.go:187-195 + vnni_amd64.s:70-73: cmb = ws*xs, term = float(isum)*cmb
-        int isum = q8_isum(b.q, b.q2, xl, xh);
-        float ws = f16_lut(b.d);
-        float cmb = ws * xs;
-        float term = cmb * (float)isum;
+        const int isum = q8_isum(b.q, b.q2, x.xl, x.xh);
+        const float cmb = f16_lut(b.d) * x.xs;
+        const float term = cmb * (float)isum;
         acc = acc + term;
     } else if (FMT == SLLM_Q4_0) {
         // q4q8.go:37-43: ws*xs*float(Σ(nib-8)·xq); Σ(nib-8)xq = Σnib·xq - 8Σxq exactly
-        int isum = nib_isum(b.q, xl, xh) - 8 * A.sx[a];
-        float ws = f16_exact(b.d);
-        float cmb = ws * xs;
-        float term = cmb * (float)isum;
+        const int isum = nib_isum(b.q, x.xl, x.xh) - 8 * x.sx;
+        const float cmb = f16_exact(b.d) * x.xs;
+        const float term = cmb * (float)isum;
         acc = acc + term;
     } else {
         // q41q8_row_amd64.s:65-71: ((float(qsum)*d) + (float(Σxq)*m)) * xs
-        const float fsx = (float)A.sx[a];
-        int qsum = nib_isum(b.q, xl, xh);
-        float t1 = (float)qsum * f16_exact(b.d);
-        float t2 = fsx * f16_exact(b.m);
+        const float fsx = (float)x.sx;
+        const int qsum = nib_isum(b.q, x.xl, x.xh);
+        const float t1 = (float)qsum * f16_exact(b.d);
+        const float t2 = fsx * f16_exact(b.m);
         float t = t1 + t2;
-        t = t * xs;
+        t = t * x.xs;
         acc = acc + t;
         if (FMT == SLLM_Q5K1) {
-            // high Q4_1 block of convertQ5KToTwoQ41: scale dh, min +0, 0/1 nibbles
-            int hsum = bits_isum(b.qh, xl, xh);
-            float h1 = (float)hsum * f16_exact(b.dh);
-            float h2 = fsx * 0.0f;
+            // high Q4_1 block of convertQ5KToTwoQ41: scale dh, min +0, 0/1 codes
+            const int hsum = bits_isum(b.qh, x.xl, x.xh);
+            const float h1 = (float)hsum * f16_exact(b.dh);
+            const float h2 = fsx * 0.0f;
             float h = h1 + h2;
-            h = h * xs;
+            h = h * x.xs;
             acc2 = acc2 + h;
         }
     }
 }
 
+// Sum over the 64 lanes of a wave with DPP moves (no LDS round trips), in a
+// fixed order: pairs, quads, 8-lane and 16-lane rows within each row of 16
+// lanes, then the four row sums (lanes 0, 16, 32, 48) added left to right.
+// Every lane receives the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+    return v + __builtin_bit_cast(float, m);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
+    v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of each 8 lanes
+    v = dpp_add<0x140>(v);  // row_mirror: the other 8 lanes of each row of 16
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return ((r0 + r1) + r2) + r3;
 }
 
-template <int FMT, int NB, int MT>
-__global__ void __launch_bounds__(1024) gemv_kernel(Planes P, const float *__restrict__ x,
-                                                    float *__restrict__ dst, int N, int G, int M, int S,
-                                                    int nbatch) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    const ActView A = carve_act(lds, FMT, MT, G);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int W = blockDim.x >> 6;
-    const int R = W / S;
-    const int row_in_batch = wave / S;
-    const int slice = wave - row_in_batch * S;
-    const int gps = (G + S - 1) / S;
-    const int g0 = slice * gps;
-    const int g1 = min(G, g0 + gps);
-
-    stage_activations<FMT>(x, M, G, A);
-    __syncthreads();
-
-    for (int bt = blockIdx.x; bt < nbatch; bt += gridDim.x) {
-        const int n = bt * R + row_in_batch;
-        float acc[MT], acc2[MT];
+template <int FMT, int NB, int D, int TPB, class NextBase>
+__device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB], const float *__restrict__ x,
+                                         int M, int G, const ActView &A, NextBase &next_base) {
+    constexpr int NV = 8 / TPB;  // float4 per thread per block
+    const int nblk = M * G;
+    const int per_pass = blockDim.x / TPB;
+    const int blk = threadIdx.x / TPB, sub = threadIdx.x % TPB;
+    if (blk < nblk) {
+        float4 xv[NV];
+        const float4 *src = (const float4 *)(x + (size_t)blk * 32) + sub * NV;
 #pragma unroll
-        for (int m = 0; m < MT; m++) acc[m] = acc2[m] = 0.0f;
-        if (n < N) {
-            BlockRegs regs[NB];
-            const size_t rowbase = (size_t)n * G;
+        for (int k = 0; k < NV; k++) xv[k] = src[k];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < NB; i++) {
-                const int g = g0 + lane + 64 * i;
-                if (g < g1) load_block<FMT>(P, rowbase + g, regs[i]);
-            }
+        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
+        __builtin_amdgcn_sched_barrier(0);
+        stage_part<FMT, TPB>(xv, blk, sub, A);
+    } else {
 #pragma unroll
-            for (int i = 0; i < NB; i++) {
-                const int g = g0 + lane + 64 * i;
-                if (g < g1) {
+        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
+    }
+    for (int b = blk + per_pass; b < nblk; b += per_pass) {
+        float4 v[NV];
+        const float4 *src = (const float4 *)(x + (size_t)b * 32) + sub * NV;
 #pragma unroll
-                    for (int m = 0; m < MT; m++)
-                        if (m < M) block_term<FMT>(regs[i], A, G, m, g, acc[m], acc2[m]);
-                }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < MT; m++) {
-            acc[m] = wave_sum(acc[m]);
-            if (FMT == SLLM_Q5K1) acc2[m] = wave_sum(acc2[m]);
-        }
-        if (S == 1) {
-            if (lane == 0 && n < N) {
-#pragma unroll
-                for (int m = 0; m < MT; m++)
-                    if (m < M) dst[(size_t)m * N + n] = (FMT == SLLM_Q5K1) ? acc[m] + acc2[m] : acc[m];
-            }
-        } else {
-            if (lane == 0) {
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    A.red[wave * 2 * MT + m] = acc[m];
-                    A.red[wave * 2 * MT + MT + m] = acc2[m];
-                }
-            }
-            __syncthreads();
-            if (slice == 0 && lane == 0 && n < N) {
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    if (m >= M) continue;
-                    float lo = A.red[wave * 2 * MT + m], hi = A.red[wave * 2 * MT + MT + m];
-                    for (int s = 1; s < S; s++) {
-                        lo = lo + A.red[(wave + s) * 2 * MT + m];
-                        hi = hi + A.red[(wave + s) * 2 * MT + MT + m];
-                    }
-                    dst[(size_t)m * N + n] = (FMT == SLLM_Q5K1) ? lo + hi : lo;
-                }
-            }
-            __syncthreads();
-        }
+        for (int k = 0; k < NV; k++) v[k] = src[k];
+        stage_part<FMT, TPB>(v, b, sub, A);
     }
 }
 
-template <int FMT, int NB, int MT>
-sllm_status launch_t(const Planes &P, const float *x, float *dst, int N, int G, int M, int S, int W,
-                     int grid, int nbatch, size_t lds, hipStream_t s) {
-    hipLaunchKernelGGL((gemv_kernel<FMT, NB, MT>), dim3(grid), dim3(W * 64), lds, s, P, x, dst, N, G, M, S,
-                       nbatch);
+// A wave's work is a stream of units: unit t is K-chunk (t % KCH) of its row
+// number (t / KCH), rows being wv, wv + TW, ... (at most RPW of them). A unit
+// is NB blocks per lane. The wave keeps D units in flight in a register ring:
+// it computes unit t, then issues the loads of unit t + D into the registers
+// it just consumed.
+template <int FMT, int NB, int D, int MT, bool HOIST>
+__global__ void __launch_bounds__(1024) gemv_kernel(Planes P, const float *__restrict__ x,
+                                                    float *__restrict__ dst, int N, int G, int M, int KCH,
+                                                    int RPW, int tpb) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
+    const ActView A = carve_act(lds, FMT, MT, G);
+    const int lane = threadIdx.x & 63;
+    const int W = blockDim.x >> 6;
+    const int TW = gridDim.x * W;
+    const int wv = blockIdx.x * W + (threadIdx.x >> 6);
+    const int U = RPW * KCH;
+    constexpr int CH = 64 * NB;  // blocks per K-chunk
+
+    // Load-stream position (row ordinal lq, chunk lk). Units past this wave's
+    // last real unit (ring padding) re-read that last unit: the data is still
+    // in flight or in cache, and no two waves pile onto the same lines.
+    const int real_rows = wv < N ? (N - 1 - wv) / TW + 1 : 0;
+    const int U_real = real_rows * KCH;
+    int lq = 0, lk = 0, lt = 0;
+    uint32_t last = (uint32_t)min(wv, N - 1) * (uint32_t)G + (uint32_t)lane;
+    auto next_base = [&]() -> uint32_t {
+        if (lt >= U_real) return last;
+        const int row = wv + lq * TW;
+        last = (uint32_t)row * (uint32_t)G + (uint32_t)(lk * CH + lane);
+        ++lt;
+        if (++lk == KCH) {
+            lk = 0;
+            ++lq;
+        }
+        return last;
+    };
+
+    BlockRegs buf[D][NB];
+    // Prologue: the activation rows (M x G blocks) are quantized by all
+    // threads, TPB lanes per block. Each thread issues its activation loads,
+    // then its wave's first D units of weights, then quantizes: it waits only
+    // for its activation loads while the weight stream is in flight.
+    switch (tpb) {
+    case 8: prologue<FMT, NB, D, 8>(P, buf, x, M, G, A, next_base); break;
+    case 4: prologue<FMT, NB, D, 4>(P, buf, x, M, G, A, next_base); break;
+    case 2: prologue<FMT, NB, D, 2>(P, buf, x, M, G, A, next_base); break;
+    default: prologue<FMT, NB, D, 1>(P, buf, x, M, G, A, next_base); break;
+    }
+    __syncthreads();
+
+    float acc[MT], acc2[MT], res[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) acc[m] = acc2[m] = res[m] = 0.0f;
+    int cq = 0, ck = 0;  // compute-stream position
+
+    // HOIST (a row is one K-chunk): every unit uses the same blocks, so the
+    // activation operands are read from LDS once, before the loop.
+    ActRegs xh[HOIST ? NB : 1][HOIST ? MT : 1];
+    if (HOIST) {
+#pragma unroll
+        for (int i = 0; i < NB; i++)
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                if (m < M) load_act<FMT>(A, (size_t)m * G + min(lane + 64 * i, G - 1), xh[HOIST ? i : 0][HOIST ? m : 0]);
+    }
+
+    // consume one unit from ring slot d
+    auto compute = [&](BlockRegs (&u)[NB]) {
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int g = ck * CH + lane + 64 * i;
+            if (g < G) {
+#pragma unroll
+                for (int m = 0; m < MT; m++) {
+                    if (m >= M) continue;
+                    if (HOIST) {
+                        block_term<FMT>(u[i], xh[HOIST ? i : 0][HOIST ? m : 0], acc[m], acc2[m]);
+                    } else {
+                        ActRegs xa;
+                        load_act<FMT>(A, (size_t)m * G + g, xa);
+                        block_term<FMT>(u[i], xa, acc[m], acc2[m]);
+                    }
+                }
+            }
+        }
+        if (++ck == KCH) {
+            // row done: reduce across the wave (fixed order), park it in lane cq
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                float v = wave_sum(acc[m]);
+                if (FMT == SLLM_Q5K1) v = v + wave_sum(acc2[m]);
+                res[m] = (lane == cq) ? v : res[m];
+                acc[m] = acc2[m] = 0.0f;
+            }
+            ck = 0;
+            ++cq;
+        }
+    };
+
+    // Ueff: units rounded up to whole rings (the tail units are clamped
+    // repeats of the last row; their results land in lanes >= RPW and are
+    // dropped). Loads are unconditional in the steady state so the compiler
+    // waits exactly for the unit being consumed.
+    const int Ueff = (U + D - 1) / D * D;
+    for (int t0 = 0; t0 + D < Ueff; t0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            compute(buf[d]);
+            load_unit<FMT, NB>(P, buf[d], next_base());
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++) compute(buf[d]);
+
+    const int row = wv + lane * TW;
+    if (lane < RPW && row < N) {
+#pragma unroll
+        for (int m = 0; m < MT; m++)
+            if (m < M) dst[(size_t)m * N + row] = res[m];
+    }
+}
+
+template <int FMT, int NB, int D, int MT>
+sllm_status launch_t(const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH, int RPW, int W,
+                     int grid, size_t lds, hipStream_t s) {
+    // hoisting needs room for the operands: not for Q5_0 (32 fp32 per block)
+    constexpr bool kCanHoist = FMT != SLLM_Q5_0 && NB * MT <= 4;
+    // lanes per activation block in the prologue: as many as the workgroup allows
+    int tpb = 8;
+    while (tpb > 1 && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
+    if (kCanHoist && KCH == 1)
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist>), dim3(grid), dim3(W * 64), lds, s, P, x, dst, N,
+                           G, M, KCH, RPW, tpb);
+    else
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false>), dim3(grid), dim3(W * 64), lds, s, P, x, dst, N, G,
+                           M, KCH, RPW, tpb);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }
 
+// D units in flight; NB * D * MT <= 8 blocks per lane.
+template <int FMT, int NB, int MT>
+sllm_status launch_d(int D, const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH, int RPW,
+                     int W, int grid, size_t lds, hipStream_t s) {
+    constexpr int DMAX = 8 / (NB * MT) >= 8 ? 8 : (8 / (NB * MT) >= 4 ? 4 : (8 / (NB * MT) >= 2 ? 2 : 1));
+    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    return launch_t<FMT, NB, 1, MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+}
+
 template <int FMT, int MT>
-sllm_status launch_nb(int NB, const Planes &P, const float *x, float *dst, int N, int G, int M, int S, int W,
-                      int grid, int nbatch, size_t lds, hipStream_t s) {
+sllm_status launch_nb(int NB, int D, const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH,
+                      int RPW, int W, int grid, size_t lds, hipStream_t s) {
     switch (NB) {
-    case 1: return launch_t<FMT, 1, MT>(P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
-    case 2: return launch_t<FMT, 2, MT>(P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
-    case 3: return launch_t<FMT, 3, MT>(P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
-    case 4: return launch_t<FMT, 4, MT>(P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
+    case 1: return launch_d<FMT, 1, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_d<FMT, 2, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 3: return launch_d<FMT, 3, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_d<FMT, 4, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 5: return launch_d<FMT, 5, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 6: return launch_d<FMT, 6, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 7: return launch_d<FMT, 7, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 8: return launch_d<FMT, 8, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported blocks-per-lane");
 }
 
 template <int FMT>
-sllm_status launch_mt(int MT, int NB, const Planes &P, const float *x, float *dst, int N, int G, int M, int S,
-                      int W, int grid, int nbatch, size_t lds, hipStream_t s) {
+sllm_status launch_mt(int MT, int NB, int D, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                      int KCH, int RPW, int W, int grid, size_t lds, hipStream_t s) {
     switch (MT) {
-    case 1: return launch_nb<FMT, 1>(NB, P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
-    case 2: return launch_nb<FMT, 2>(NB, P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
-    case 4: return launch_nb<FMT, 4>(NB, P, x, dst, N, G, M, S, W, grid, nbatch, lds, s);
+    case 1: return launch_nb<FMT, 1>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_nb<FMT, 2>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_nb<FMT, 4>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported row tile");
 }
 
 constexpr size_t kMaxLds = 64 * 1024;
 
+int device_cus() {
+    static thread_local int dev = -1, cus = 0;
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) return 256;
+    if (d != dev) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || v <= 0) v = 256;
+        dev = d;
+        cus = v;
+    }
+    return cus;
+}
+
 }  // namespace
 
-// Launch shape: W waves per workgroup; S waves per weight row (K split), so a
-// workgroup covers R = W/S rows per batch; NB blocks per lane (<= 4).
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         hipStream_t s) {
     if (N <= 0 || G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
     const Tuning &T = tuning();
-    const int W = T.gemv_waves;
-    // K split: enough row batches to fill the device, but never below 64 blocks
-    // per wave, and at most 4 blocks per lane.
-    int S = 1;
-    const int s_cap = G >= 64 ? (G / 64 < W ? G / 64 : W) : 1;
-    while (S * 2 <= s_cap && ((int64_t)N * S + W - 1) / W < T.gemv_min_batches) S *= 2;
-    while ((G + 64 * S - 1) / (64 * S) > 4 && S * 2 <= W) S *= 2;
-    const int NB = (G + 64 * S - 1) / (64 * S);
-    if (NB > 4) return set_error(SLLM_ERR_SHAPE, "gemv: cols too large for the decode kernel");
-    const int R = W / S;
-    const int nbatch = (N + R - 1) / R;
-    const int grid = nbatch < T.gemv_grid_cap ? nbatch : T.gemv_grid_cap;
-    // Activation rows per launch, limited by LDS.
+    const int cus = device_cus();
+    // Blocks per lane per unit. Rows of up to 8 x 64 blocks are one unit
+    // (one K-chunk, issued at once); longer rows are split into K-chunks of
+    // the largest lane-group count <= 8 that divides them (no partial chunks).
+    const int lg = (G + 63) / 64;
+    const int nb_cap = T.gemv_max_nb;
+    int NB = lg;
+    if (lg > nb_cap) {
+        NB = nb_cap;
+        while (NB > 1 && lg % NB) NB--;
+        if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
+    }
+    const int KCH = (G + 64 * NB - 1) / (64 * NB);
+    int W = T.gemv_waves;
+    while (W > 4 && (int64_t)(W / 2) * cus * T.gemv_wg_per_cu >= N) W /= 2;  // small row counts: more CUs
+    // rows per wave for one pass over the device, then just enough waves for
+    // that many rows each (every wave gets RPW rows, at most W - 1 spare)
+    const int64_t slots = (int64_t)cus * T.gemv_wg_per_cu * W;
+    const int RPW = (int)((N + slots - 1) / slots);
+    if (RPW > 64) return set_error(SLLM_ERR_SHAPE, "gemv: more than 64 rows per wave (rows too many)");
+    const int64_t waves = ((int64_t)N + RPW - 1) / RPW;
+    const int grid = (int)((waves + W - 1) / W);
+    const int U = RPW * KCH;
     int done = 0;
     while (done < M) {
-        int left = M - done;
+        const int left = M - done;
         int MT = left >= 4 ? 4 : (left >= 2 ? 2 : 1);
         while (MT > 1 && act_lds_bytes(fmt, MT, G) > kMaxLds) MT >>= 1;
         if (act_lds_bytes(fmt, MT, G) > kMaxLds)
             return set_error(SLLM_ERR_SHAPE, "gemv: activation row does not fit in LDS");
+        // ring depth: units in flight per wave, bounded by registers (NB*D*MT
+        // <= 8 blocks per lane), by the wave's unit count, and by the bytes in
+        // flight over the whole device (enough to cover HBM latency; more only
+        // piles compute into the tail)
+        const int64_t unit_bytes = (int64_t)64 * NB * plane_block_bytes(fmt);
+        const int64_t inflight = (int64_t)T.gemv_inflight_kb * 1024;
+        int D = 1;
+        while (D * 2 * NB * MT <= 8 && D < U && (int64_t)waves * unit_bytes * D * 2 <= inflight) D *= 2;
         const int mrows = left < MT ? left : MT;
         const size_t lds = act_lds_bytes(fmt, MT, G);
         const float *xp = x + (size_t)done * G * 32;
         float *dp = dst + (size_t)done * N;
         sllm_status st;
         switch (fmt) {
-        case SLLM_Q8_0: st = launch_mt<SLLM_Q8_0>(MT, NB, P, xp, dp, N, G, mrows, S, W, grid, nbatch, lds, s); break;
-        case SLLM_Q4_0: st = launch_mt<SLLM_Q4_0>(MT, NB, P, xp, dp, N, G, mrows, S, W, grid, nbatch, lds, s); break;
-        case SLLM_Q4_1: st = launch_mt<SLLM_Q4_1>(MT, NB, P, xp, dp, N, G, mrows, S, W, grid, nbatch, lds, s); break;
-        case SLLM_Q5_0: st = launch_mt<SLLM_Q5_0>(MT, NB, P, xp, dp, N, G, mrows, S, W, grid, nbatch, lds, s); break;
-        case SLLM_Q5K1: st = launch_mt<SLLM_Q5K1>(MT, NB, P, xp, dp, N, G, mrows, S, W, grid, nbatch, lds, s); break;
+        case SLLM_Q8_0: st = launch_mt<SLLM_Q8_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q4_0: st = launch_mt<SLLM_Q4_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q4_1: st = launch_mt<SLLM_Q4_1>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q5_0: st = launch_mt<SLLM_Q5_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q5K1: st = launch_mt<SLLM_Q5K1>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");
         }
         if (st != SLLM_OK) return st;
@@ -319,15 +497,16 @@ namespace {
 
 __global__ void quantize_act_kernel(const float *__restrict__ x, int nblocks, int8_t *__restrict__ xq,
                                     float *__restrict__ xs, int32_t *__restrict__ sx) {
-    // Same device routine as the GEMV/GEMM prologue; 8 lanes per block.
+    // The GEMV prologue routine with 8 lanes per 32-element block (one float4 each).
     const int total = nblocks * 8;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
         const int blk = i >> 3, sub = i & 7;
-        const float4 v = *(const float4 *)(x + (size_t)blk * 32 + sub * 4);
+        const float4 v[1] = {*((const float4 *)(x + (size_t)blk * 32) + sub)};
+        int w[1];
         float s;
         int sm;
-        uint32_t packed = quantize_quarter(v, &s, &sm);
-        *(uint32_t *)(xq + (size_t)blk * 32 + sub * 4) = packed;
+        quantize_part<8>(v, w, s, sm);
+        ((int *)(xq + (size_t)blk * 32))[sub] = w[0];
         if (sub == 0) {
             xs[blk] = s;
             if (sx) sx[blk] = sm;
@@ -338,43 +517,38 @@ __global__ void quantize_act_kernel(const float *__restrict__ x, int nblocks, in
 template <int FMT>
 __global__ void block_dots_kernel(Planes P, const float *__restrict__ x, int N, int G, int M,
                                   int32_t *__restrict__ out) {
-    // One thread per (m, n, g); activations quantized on the fly by the 8-lane
-    // routine (each thread of an 8-group handles one quarter of block g).
+    // One thread per (m, n, g); the activation block is quantized with the
+    // prologue routine, the block dot with the GEMV's block routine.
     const int64_t total = (int64_t)M * N * G;
-    for (int64_t t = (int64_t)blockIdx.x * (blockDim.x / 8) + (threadIdx.x >> 3); t < total;
-         t += (int64_t)gridDim.x * (blockDim.x / 8)) {
-        const int sub = threadIdx.x & 7;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+         t += (int64_t)gridDim.x * blockDim.x) {
         const int g = (int)(t % G);
         const int n = (int)((t / G) % N);
         const int m = (int)(t / ((int64_t)G * N));
-        const float *xb = x + ((size_t)m * G + g) * 32;
-        const float4 v = *(const float4 *)(xb + sub * 4);
+        const float4 *xb = (const float4 *)(x + ((size_t)m * G + g) * 32);
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = xb[k];
+        const size_t idx = (size_t)n * G + g;
+        if (FMT == SLLM_Q5_0) {
+            const float sum = q5_block_sum(P.qs[idx], P.qh[idx], v);
+            out[t] = __builtin_bit_cast(int32_t, sum);
+            continue;
+        }
+        int w[8];
         float s;
         int sm;
-        uint32_t packed = quantize_quarter(v, &s, &sm);
-        // gather the 8 packed quarters of the block into every lane
-        int w[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) w[k] = __shfl((int)packed, (threadIdx.x & ~7) + k);
-        if (sub != 0) continue;
-        const int4 xl = make_int4(w[0], w[1], w[2], w[3]);
-        const int4 xh = make_int4(w[4], w[5], w[6], w[7]);
-        const size_t idx = (size_t)n * G + g;
+        quantize_part<1>(v, w, s, sm);
+        const int4 xl = make_int4(w[0], w[1], w[2], w[3]), xh = make_int4(w[4], w[5], w[6], w[7]);
         if (FMT == SLLM_Q8_0) {
             out[t] = q8_isum(P.qs[idx], P.qs2[idx], xl, xh);
         } else if (FMT == SLLM_Q4_0) {
             out[t] = nib_isum(P.qs[idx], xl, xh) - 8 * sm;
         } else if (FMT == SLLM_Q4_1) {
             out[t] = nib_isum(P.qs[idx], xl, xh);
-        } else if (FMT == SLLM_Q5K1) {
+        } else {
             out[2 * t] = nib_isum(P.qs[idx], xl, xh);
             out[2 * t + 1] = bits_isum(P.qh[idx], xl, xh);
-        } else {
-            float4 xv[8];
-#pragma unroll
-            for (int k = 0; k < 8; k++) xv[k] = ((const float4 *)xb)[k];
-            float sum = q5_block_sum(P.qs[idx], P.qh[idx], xv);
-            out[t] = __builtin_bit_cast(int32_t, sum);
         }
     }
 }
@@ -434,7 +608,7 @@ sllm_status launch_quantize_act(const float *x, int rows, int G, int8_t *xq, flo
 sllm_status launch_block_dots(int fmt, const Planes &P, const float *x, int N, int G, int M, int32_t *out,
                               hipStream_t s) {
     int64_t total = (int64_t)M * N * G;
-    int64_t grid64 = (total + 31) / 32;
+    int64_t grid64 = (total + 255) / 256;
     int grid = grid64 > 8192 ? 8192 : (int)grid64;
     switch (fmt) {
     case SLLM_Q8_0: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q8_0>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;

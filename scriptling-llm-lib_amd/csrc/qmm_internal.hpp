@@ -62,6 +62,10 @@ inline int raw_block_bytes(int fmt) {
     return 0;
 }
 
+// Spare blocks at the end of every plane (the GEMV reads whole 64-block lane
+// groups and may run up to 8 x 64 blocks past the last row's end).
+constexpr int kPlanePadBlocks = 8 * 64;
+
 // Carve the planes of a (rows x groups) weight of format fmt out of `base`
 // (nullptr: only compute the size). Returns the total allocation size.
 size_t carve_planes(int fmt, int64_t nblocks, void *base, MutPlanes *out);
@@ -103,9 +107,10 @@ sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlane
 
 // Tuning parameters (launch shapes), settable through sllm_set_param.
 struct Tuning {
-    int gemv_grid_cap = 1024;  // max workgroups of a GEMV launch
-    int gemv_waves = 8;        // waves per GEMV workgroup (4, 8 or 16)
-    int gemv_min_batches = 512;// split K until at least this many row batches
+    int gemv_waves = 16;       // waves per GEMV workgroup (4, 8 or 16); fewer for small row counts
+    int gemv_wg_per_cu = 1;    // GEMV workgroups per CU (persistent grid = CUs x this)
+    int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
+    int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
 };
 Tuning &tuning();

@@ -23,13 +23,17 @@ size_t carve_planes(int fmt, int64_t nb, void *base, MutPlanes *out) {
         off += bytes;
         return p;
     };
+    // kPlanePadBlocks spare entries per plane: a GEMV lane may read up to one
+    // K-chunk past a row's last block (the values are ignored), so the last row
+    // of a plane must not run off the allocation.
+    const size_t n = (size_t)nb + kPlanePadBlocks;
     MutPlanes p;
-    p.qs = (int4 *)take((size_t)nb * 16);
-    if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take((size_t)nb * 16);
-    if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take((size_t)nb * 4);
-    p.d = (uint16_t *)take((size_t)nb * 2);
-    if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1) p.m = (uint16_t *)take((size_t)nb * 2);
-    if (fmt == SLLM_Q5K1) p.dh = (uint16_t *)take((size_t)nb * 2);
+    p.qs = (int4 *)take(n * 16);
+    if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take(n * 16);
+    if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take(n * 4);
+    p.d = (uint16_t *)take(n * 2);
+    if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1) p.m = (uint16_t *)take(n * 2);
+    if (fmt == SLLM_Q5K1) p.dh = (uint16_t *)take(n * 2);
     if (out) *out = p;
     return (off + 255) & ~(size_t)255;
 }
