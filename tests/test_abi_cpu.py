@@ -1,0 +1,68 @@
+"""The C ABI on the CPU: the library loads, exports every symbol the header
+declares, and rejects bad arguments with status codes before touching a GPU."""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import sllm_qmm as sq
+
+
+def test_library_exports_every_declared_symbol():
+    names = sq.exported_names()
+    assert len(names) >= 15
+    lib = sq.lib()
+    for n in names:
+        assert hasattr(lib, n), n
+    # and nothing else under the sllm_ prefix is exported by accident
+    out = subprocess.run(["nm", "-D", "--defined-only", sq.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-1].startswith("sllm_")}
+    assert exported == set(names)
+
+
+def test_kernel_info_names_the_target():
+    assert "gfx950" in sq.kernel_info()
+
+
+def _status(fn, *args):
+    return fn(*args)
+
+
+def test_argument_errors_need_no_device():
+    lib = sq.lib()
+    raw = np.zeros(34 * 4, np.uint8)
+    h = C.c_void_p()
+    p = raw.ctypes.data
+    assert lib.sllm_weight_from_quant(b"q9", p, raw.nbytes, 1, 4, 32, C.byref(h)) == 2      # unknown QType
+    assert "q9" in lib.sllm_last_error().decode()
+    assert lib.sllm_weight_from_quant(b"q8", p, raw.nbytes, 1, 4, 33, C.byref(h)) == 3      # cols % 32
+    assert lib.sllm_weight_from_quant(b"q8", p, raw.nbytes, 2, 4, 32, C.byref(h)) == 1      # groups != cols/32
+    assert lib.sllm_weight_from_quant(b"q8", p, 10, 1, 4, 32, C.byref(h)) == 1              # Raw too short
+    assert lib.sllm_weight_from_quant(b"q8", None, 10, 1, 4, 32, C.byref(h)) == 1           # null Raw
+    assert lib.sllm_weight_from_gguf(10, p, raw.nbytes, 4, 256, C.byref(h)) == 2            # Q2_K: dense in the reference
+    assert lib.sllm_weight_from_gguf(12, p, raw.nbytes, 4, 128, C.byref(h)) == 3            # Q4_K needs cols % 256
+    assert lib.sllm_weight_from_gguf(12, p, 16, 1, 256, C.byref(h)) == 1                    # too short
+    assert lib.sllm_matmul_quant_into_f32(None, p, 1, 32, p) == 1
+    assert lib.sllm_set_param(b"no_such_knob", 3) == 1
+
+
+@pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
+def test_no_gpu_is_a_device_error_not_a_fallback():
+    lib = sq.lib()
+    assert lib.sllm_init() == 4
+    assert "gfx950" in lib.sllm_last_error().decode() or "device" in lib.sllm_last_error().decode()
+    raw = np.zeros(34, np.uint8)
+    h = C.c_void_p()
+    assert lib.sllm_weight_from_quant(b"q8", raw.ctypes.data, 34, 1, 1, 32, C.byref(h)) == 4
+    with pytest.raises(sq.SllmError) as e:
+        sq.DeviceWeight.from_quant(sq.QuantWeight("q8", raw, 1, 1, 32))
+    assert e.value.status == 4
+
+
+def test_python_host_mirror_names():
+    # the Go entry points this path replaces, mirrored by the host module
+    for name in ("QuantWeight", "load_weight_f32_direct", "quantize_q8_rows_f32",
+                 "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev"):
+        assert hasattr(sq, name)
