@@ -48,6 +48,31 @@ struct Ws {
 };
 std::unordered_map<uint64_t, Ws> g_ws;
 
+// The GEMM activation workspace of `stream` on the current device, grown to at
+// least `need` bytes. Growing synchronizes the stream before freeing the old
+// buffer (work already queued on it may still read it).
+sllm_status workspace(hipStream_t stream, size_t need, void **out, size_t *cap) {
+    int dev = 0;
+    SLLM_HIP(hipGetDevice(&dev));
+    const uint64_t key = ((uint64_t)(uintptr_t)stream << 8) ^ (uint64_t)dev;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Ws &w = g_ws[key];
+    if (w.cap < need) {
+        if (w.p) {
+            SLLM_HIP(hipStreamSynchronize(stream));
+            (void)hipFree(w.p);
+            w.p = nullptr;
+            w.cap = 0;
+        }
+        size_t want = need < ((size_t)4 << 20) ? ((size_t)4 << 20) : need;
+        if (hipMalloc(&w.p, want) != hipSuccess) return set_error(SLLM_ERR_OOM, "GEMM workspace allocation failed");
+        w.cap = want;
+    }
+    *out = w.p;
+    *cap = w.cap;
+    return SLLM_OK;
+}
+
 sllm_status ensure_init() {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_init_done) {
@@ -400,7 +425,14 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, in
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     Planes P = as_const(w->planes);
-    return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    if (x_rows < tuning().gemm_min_rows || w->fmt == SLLM_Q5_0)
+        return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    // GEMM: quantized activations go to a per-(device, stream) workspace
+    const size_t need = gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows);
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, need, &ws, &cap)) != SLLM_OK) return st;
+    return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
 }
 
 sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int x_rows, int x_cols, float *dst) {

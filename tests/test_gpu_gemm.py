@@ -1,0 +1,91 @@
+"""GPU parity of the prefill path (xRows >= 64: int8 MFMA GEMM; Q5_0 stays on
+the GEMV) against the oracle, including full BASELINE C4 shapes checked on a
+row subset (weight rows are independent, so a row slice of the Raw bytes is
+the oracle's input for those output columns)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+import sllm_qmm as sq
+from sllm_qmm import synth
+
+from _helpers import assert_fp32_parity, make_raw, make_x, term_abs_sum
+
+pytestmark = pytest.mark.gpu
+
+QTYPES = ["q8", "q4", "q4_1", "q5k1", "q5"]
+
+
+def slice_rows(qtype: str, raw: np.ndarray, N: int, G: int, rows: np.ndarray) -> np.ndarray:
+    """Raw bytes of the given weight rows (QuantWeight.Raw layout)."""
+    if qtype == "q5k1":
+        lo = raw[: N * G * 20].reshape(N, G * 20)[rows]
+        hi = raw[N * G * 20:].reshape(N, G * 20)[rows]
+        return np.concatenate([lo.reshape(-1), hi.reshape(-1)])
+    bb = oracle.BLOCK_BYTES[qtype]
+    return raw.reshape(N, G * bb)[rows].reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", QTYPES)
+@pytest.mark.parametrize("M", [64, 65, 130])
+@pytest.mark.parametrize("N,K", [(96, 512), (200, 1024)])
+def test_prefill_parity(qtype, M, N, K):
+    if qtype == "q5k1" and K % 256:
+        pytest.skip("Q5_K rows are whole super-blocks")
+    raw = make_raw(qtype, N, K, seed=M + N)
+    x = make_x(M, K, seed=K)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} M={M} {N}x{K}")
+
+
+@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1"])
+def test_prefill_edge_activations(qtype):
+    # zero rows, denormal rows and huge rows through the GEMM's quantize pre-pass
+    N, K, M = 64, 512, 64
+    raw = make_raw(qtype, N, K, seed=5)
+    x = make_x(M, K, seed=6)
+    x[0] = 0.0
+    x[1] *= np.float32(1e-39)
+    x[2] *= np.float32(1e30)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} edges")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("ggml_type,N,K,M", [
+    (13, 4096, 4096, 64),      # C4 Q5_K q/o projection, M = 64
+    (13, 1024, 4096, 512),     # C4 Q5_K k/v projection, M = 512
+    (12, 14336, 4096, 64),     # C3 Q4_K gate/up, M = 64
+    (6, 4096, 4096, 64),       # C4 Q5_0 (GEMV path)
+])
+def test_prefill_full_shapes_on_row_subset(ggml_type, N, K, M):
+    raw_gguf = synth.gguf_tensor(ggml_type, 7, N, K)
+    w = sq.load_weight_f32_direct(ggml_type, raw_gguf, N, K)
+    raw = w.export()
+    x = make_x(M, K, seed=9)
+    got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    got = got.reshape(M, N)
+    rows = np.unique(np.concatenate([np.arange(32), np.arange(N - 32, N),
+                                     np.random.default_rng(0).integers(0, N, 64)]))
+    sub = slice_rows(w.qtype, raw, N, K // 32, rows)
+    ref = oracle.matmul(w.qtype, sub, rows.size, x)
+    assert_fp32_parity(got[:, rows], ref, term_abs_sum(w.qtype, sub, rows.size, x), f"{w.qtype} {N}x{K} M={M}")
+
+
+def test_gemm_rows_match_gemv_rows():
+    # the same activation row through the GEMM (inside a 64-row batch) and the
+    # GEMV (alone) gives the same per-block terms; sums may differ only by order
+    N, K = 256, 2048
+    raw = make_raw("q4_1", N, K, seed=3)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight("q4_1", raw, K // 32, N, K))
+    x = make_x(64, K, seed=4)
+    big, _, _ = sq.model_matmul_quant_into_f32(w, x, 64, K)
+    one = sq.model_matmul_row_quant_into_f32(w, x[17])
+    bound = term_abs_sum("q4_1", raw, N, x[17:18])[0]
+    assert np.all(np.abs(big.reshape(64, N)[17].astype(np.float64) - one) <= 2e-5 * bound + 1e-30)
