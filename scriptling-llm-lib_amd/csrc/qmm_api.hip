@@ -425,7 +425,7 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, in
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     Planes P = as_const(w->planes);
-    if (x_rows < tuning().gemm_min_rows || w->fmt == SLLM_Q5_0)
+    if (x_rows < tuning().gemm_min_rows || !gemm_supported(w->fmt, w->groups))
         return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
     // GEMM: quantized activations go to a per-(device, stream) workspace
     const size_t need = gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows);

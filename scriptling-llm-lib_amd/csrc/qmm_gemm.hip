@@ -1,21 +1,26 @@
 // Prefill GEMM (xRows >= 64) on the int8 matrix cores.
 //
 // 1. The activation rows are quantized once into a workspace (xq int8 [M][K],
-//    xs fp32 [M][G], Σxq int32 [M][G]) by the same routine as the GEMV prologue.
-// 2. Each workgroup computes a 64 (activation rows) x 64 (weight rows) tile of
-//    dst. For every 32-element block g, wave w runs v_mfma_i32_16x16x32_i8 on
-//    its 16 activation rows against four 16-row slices of the weight tile:
-//    K = 32 is exactly one block, so each MFMA returns the exact int32 block
-//    dots (the reference's isum / qsum) for a 16 x 16 sub-tile. The epilogue
-//    then forms the reference's per-block fp32 term from them, as the GEMV does,
-//    and accumulates it.
+//    xs fp32 [M][G], Σxq int32 [M][G]) by the GEMV prologue's routine.
+// 2. A workgroup of 2 x WN waves computes a 64 x BN tile of dst (64
+//    activation rows x BN = 32 WN weight rows), each wave a 32 x 32 sub-tile.
+//    K is staged KB blocks at a time through LDS, double-buffered: the global
+//    loads of stage s+1 are in flight while stage s is computed. Per 32-element
+//    block each wave runs v_mfma_i32_16x16x32_i8 on its four 16 x 16 pieces:
+//    K = 32 is exactly one block, so every MFMA returns exact int32 block dots
+//    (the reference's isum / qsum). The epilogue forms the reference's
+//    per-block fp32 term from them, exactly as the GEMV does, and accumulates.
+// 3. When there are too few tiles to fill the device, K is split over S
+//    workgroups; each writes its partial tile and a second kernel adds the S
+//    partials in split order (fixed order: results are reproducible).
 //
-// MFMA operand layout (16x16x32 i8): A[i][k] sits in lane i + 16 (k / 8), byte
+// MFMA operand layout (16x16x32 i8): A[i][k] in lane i + 16 (k / 8), byte
 // k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4),
 // element i % 4.
 //
-// Roofline: the per-block fp32 epilogue (3-6 VALU ops per output per 32 MACs)
-// bounds this kernel, not the matrix cores or HBM.
+// Roofline: the per-block fp32 epilogue (4-6 VALU ops per output per 32 MACs)
+// bounds this kernel, not the matrix cores (which it keeps about 10 % busy) or,
+// from M ~ 64 up, HBM.
 #include <hip/hip_runtime.h>
 
 #include "qmm_device.hpp"
@@ -27,161 +32,402 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 64;  // activation rows per workgroup (4 waves x 16)
-constexpr int kBN = 64;  // weight rows per workgroup (4 MFMA column tiles)
+constexpr int kBM = 64;   // activation rows per workgroup
+constexpr int kKB = 4;    // blocks (x 32 elements) per K stage
+constexpr int kARow = kKB * 32 + 8;  // LDS bytes per activation row (padded: conflict-free b64 reads)
 
-// B operand: 8 consecutive elements (chunk c = 0..3 of the block) of weight
-// row `row`, block g, as 8 int8 codes (Q4: unsigned nibbles; Q5K1 high: 0/1).
+// Bytes of weight codes per block in LDS, per format.
 template <int FMT>
-__device__ __forceinline__ long b_frag(const Planes &P, size_t idx, int c) {
-    if (FMT == SLLM_Q8_0) {
-        const int4 *plane = (c < 2) ? P.qs : P.qs2;
-        const long *p = (const long *)(plane + idx);
-        return p[c & 1];
+constexpr int wcode_bytes() {
+    return FMT == SLLM_Q8_0 ? 32 : 16;
+}
+template <int FMT>
+constexpr int brow_bytes() {
+    return kKB * wcode_bytes<FMT>() + 8;  // padded
+}
+
+template <int FMT, int BN>
+struct alignas(16) Stage {
+    // LDS image of one K stage
+    int8_t a[kBM * kARow];                       // activation codes
+    int8_t b[BN * brow_bytes<FMT>()];            // weight codes
+    float xs[kKB][kBM];                          // activation scales
+    int sx[kKB][kBM];                            // Σxq
+    uint16_t d[kKB][BN];                         // weight scales
+    uint16_t m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? kKB : 1][BN];
+    uint16_t dh[FMT == SLLM_Q5K1 ? kKB : 1][BN];
+    uint32_t hb[FMT == SLLM_Q5K1 ? kKB : 1][BN];
+};
+
+// Global -> register staging of one K stage (issued before the compute of the
+// previous stage, stored to LDS after it). T threads.
+template <int FMT, int BN, int T>
+struct Fetch {
+    static constexpr int A_N = kBM * kKB * 32 / 16;              // int4 of activation codes
+    static constexpr int B_N = BN * kKB * wcode_bytes<FMT>() / 16; // int4 of weight codes
+    static constexpr int S_N = kKB * kBM;                         // activation scalars
+    static constexpr int W_N = kKB * BN;                          // weight scalars
+    static constexpr int A_PER = (A_N + T - 1) / T, B_PER = (B_N + T - 1) / T;
+    static constexpr int S_PER = (S_N + T - 1) / T, W_PER = (W_N + T - 1) / T;
+    int4 a[A_PER];
+    int4 b[B_PER];
+    float xs[S_PER];
+    int sx[S_PER];
+    uint16_t d[W_PER], m[W_PER], dh[W_PER];
+    uint32_t hb[W_PER];
+};
+
+template <int FMT, int BN, int T>
+__device__ __forceinline__ void fetch_stage(Fetch<FMT, BN, T> &f, const Planes &P, const int8_t *__restrict__ xq,
+                                            const float *__restrict__ xs, const int *__restrict__ sx, int m0,
+                                            int n0, int M, int N, int G, int g0) {
+    using F = Fetch<FMT, BN, T>;
+    const int tid = threadIdx.x;
+    const int K = G * 32;
+    constexpr int A_ROW_INT4 = kKB * 2;
+#pragma unroll
+    for (int i = 0; i < F::A_PER; i++) {
+        const int e = tid + T * i;
+        if (F::A_N % T == 0 || e < F::A_N) {
+            const int r = e / A_ROW_INT4, c = e % A_ROW_INT4;
+            const int m = min(m0 + r, M - 1);
+            f.a[i] = *(const int4 *)(xq + (size_t)m * K + (size_t)g0 * 32 + c * 16);
+        }
     }
-    // 4-bit formats: byte i = element i (low nibble) | element i+16 (high)
-    const long v = ((const long *)(P.qs + idx))[c & 1];
+    constexpr int WB = wcode_bytes<FMT>() / 16;  // int4 per block (2 for Q8_0: qs, qs2)
+#pragma unroll
+    for (int i = 0; i < F::B_PER; i++) {
+        const int e = tid + T * i;
+        if (F::B_N % T == 0 || e < F::B_N) {
+            const int r = e / (kKB * WB), rem = e % (kKB * WB);
+            const int blk = rem / WB, half = rem % WB;
+            const int n = min(n0 + r, N - 1);
+            const size_t idx = (size_t)n * G + g0 + blk;
+            f.b[i] = (FMT == SLLM_Q8_0 && half) ? P.qs2[idx] : P.qs[idx];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < F::S_PER; i++) {
+        const int e = tid + T * i;
+        if (F::S_N % T == 0 || e < F::S_N) {
+            const int blk = e / kBM, r = e % kBM;
+            const int m = min(m0 + r, M - 1);
+            f.xs[i] = xs[(size_t)m * G + g0 + blk];
+            f.sx[i] = sx[(size_t)m * G + g0 + blk];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < F::W_PER; i++) {
+        const int e = tid + T * i;
+        if (F::W_N % T == 0 || e < F::W_N) {
+            const int blk = e / BN, c = e % BN;
+            const int n = min(n0 + c, N - 1);
+            const size_t idx = (size_t)n * G + g0 + blk;
+            f.d[i] = P.d[idx];
+            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) f.m[i] = P.m[idx];
+            if (FMT == SLLM_Q5K1) {
+                f.dh[i] = P.dh[idx];
+                f.hb[i] = P.qh[idx];
+            }
+        }
+    }
+}
+
+template <int FMT, int BN, int T>
+__device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FMT, BN> &S) {
+    using F = Fetch<FMT, BN, T>;
+    const int tid = threadIdx.x;
+    constexpr int A_ROW_INT4 = kKB * 2;
+#pragma unroll
+    for (int i = 0; i < F::A_PER; i++) {
+        const int e = tid + T * i;
+        if (F::A_N % T == 0 || e < F::A_N) {
+            const int r = e / A_ROW_INT4, c = e % A_ROW_INT4;
+            int2 *p = (int2 *)(S.a + r * kARow + c * 16);  // padded rows: 8-byte aligned
+            p[0] = make_int2(f.a[i].x, f.a[i].y);
+            p[1] = make_int2(f.a[i].z, f.a[i].w);
+        }
+    }
+    constexpr int WB = wcode_bytes<FMT>() / 16;
+#pragma unroll
+    for (int i = 0; i < F::B_PER; i++) {
+        const int e = tid + T * i;
+        if (F::B_N % T == 0 || e < F::B_N) {
+            const int r = e / (kKB * WB), rem = e % (kKB * WB);
+            const int blk = rem / WB, half = rem % WB;
+            int2 *p = (int2 *)(S.b + r * brow_bytes<FMT>() + blk * wcode_bytes<FMT>() + half * 16);
+            p[0] = make_int2(f.b[i].x, f.b[i].y);
+            p[1] = make_int2(f.b[i].z, f.b[i].w);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < F::S_PER; i++) {
+        const int e = tid + T * i;
+        if (F::S_N % T == 0 || e < F::S_N) {
+            const int blk = e / kBM, r = e % kBM;
+            S.xs[blk][r] = f.xs[i];
+            S.sx[blk][r] = f.sx[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < F::W_PER; i++) {
+        const int e = tid + T * i;
+        if (F::W_N % T == 0 || e < F::W_N) {
+            const int blk = e / BN, c = e % BN;
+            S.d[blk][c] = f.d[i];
+            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][c] = f.m[i];
+            if (FMT == SLLM_Q5K1) {
+                S.dh[FMT == SLLM_Q5K1 ? blk : 0][c] = f.dh[i];
+                S.hb[FMT == SLLM_Q5K1 ? blk : 0][c] = f.hb[i];
+            }
+        }
+    }
+}
+
+// B operand from LDS: 8 codes (chunk c of the block) of weight row `row`.
+template <int FMT, int BN>
+__device__ __forceinline__ long b_frag(const Stage<FMT, BN> &S, int row, int blk, int c) {
+    const int8_t *base = S.b + row * brow_bytes<FMT>() + blk * wcode_bytes<FMT>();
+    if (FMT == SLLM_Q8_0) return *(const long *)(base + c * 8);
+    const long v = *(const long *)(base + (c & 1) * 8);
     const long lo = 0x0f0f0f0f0f0f0f0fL;
     return (c < 2) ? (v & lo) : ((v >> 4) & lo);
 }
 
-// High-bit operand of Q5K1: elements 8c..8c+7 of the 32-bit mask as 0/1 bytes.
+// Q5K1 high operand: elements 8c..8c+7 of the mask as 0/1 bytes.
 __device__ __forceinline__ long bits_frag(uint32_t hb, int c) {
     const uint32_t t = hb >> (8 * c);
-    const uint32_t lo = (uint32_t)spread4(t);
-    const uint32_t hi = (uint32_t)spread4(t >> 4);
-    return (long)((uint64_t)lo | ((uint64_t)hi << 32));
+    return (long)((uint64_t)(uint32_t)spread4(t) | ((uint64_t)(uint32_t)spread4(t >> 4) << 32));
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(256) gemm_kernel(Planes P, const int8_t *__restrict__ xq,
-                                                   const float *__restrict__ xs, const int *__restrict__ sx,
-                                                   float *__restrict__ dst, int M, int N, int G, int mtiles,
-                                                   int ntiles) {
+// Workgroup = 2 x WN waves; tile 64 x BN (BN = 32 WN); K stages [st0, st1).
+template <int FMT, int WN>
+__global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *__restrict__ xq,
+                                                        const float *__restrict__ xs, const int *__restrict__ sx,
+                                                        float *__restrict__ out, int M, int N, int G, int mtiles,
+                                                        int ntiles, int splits, int sps) {
+    constexpr int BN = 32 * WN, T = 128 * WN;
+    constexpr bool DUAL = FMT == SLLM_Q5K1;
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+    Stage<FMT, BN> *stages = (Stage<FMT, BN> *)lds_raw;
+
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int K = G * 32;
-    // XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs;
-    // tile t = (id / 8) + (id % 8) * per_xcd keeps the M-tiles of one weight
-    // tile on one XCD, so its weight rows come from HBM once into that L2.
-    const int total = mtiles * ntiles;
+    const int wm = wave & 1, wn = wave >> 1;
+    // XCD-aware order: workgroup id -> XCD (id % 8); consecutive linear indices
+    // (the M-tiles of one weight tile and split) stay on one XCD, so that
+    // weight tile comes from HBM once into that XCD's L2.
+    const int total = mtiles * ntiles * splits;
     const int per_xcd = (total + 7) / 8;
-    const int id = blockIdx.x;
-    const int t = (id % 8) * per_xcd + id / 8;
-    if (t >= total) return;
-    const int mt = t % mtiles, nt = t / mtiles;
+    const int lin = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (lin >= total) return;
+    const int mt = lin % mtiles;
+    const int rest = lin / mtiles;
+    const int sp = rest % splits, nt = rest / splits;
+    const int m0 = mt * kBM, n0 = nt * BN;
     const int r16 = lane & 15, c4 = lane >> 4;
-    const int m_a = min(mt * kBM + wave * 16 + r16, M - 1);  // A-operand row (clamped; discarded if >= M)
-    const int m_o = mt * kBM + wave * 16 + 4 * c4;           // first of this lane's 4 output rows
-    size_t nidx[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) nidx[j] = (size_t)min(nt * kBN + 16 * j + r16, N - 1) * G;
+    const int nst = G / kKB;
+    const int st0 = sp * sps, st1 = min(nst, st0 + sps);
 
-    float acc[4][4], acc2[4][4];
+    float acc[2][2][4], acc2[DUAL ? 2 : 1][DUAL ? 2 : 1][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[j][r] = acc2[j][r] = 0.0f;
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                acc[i][j][r] = 0.0f;
+                acc2[DUAL ? i : 0][DUAL ? j : 0][r] = 0.0f;
+            }
 
-    const int8_t *arow = xq + (size_t)m_a * K + c4 * 8;
-    for (int g = 0; g < G; g++) {
-        const long a = *(const long *)(arow + (size_t)g * 32);
-        float xsr[4], fsx[4];
-        int sxr[4];
+    Fetch<FMT, BN, T> f;
+    if (st0 < st1) {
+        fetch_stage<FMT, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * kKB);
+        store_stage<FMT, BN, T>(f, stages[0]);
+    }
+    __syncthreads();
+
+    for (int s = st0; s < st1; s++) {
+        if (s + 1 < st1) fetch_stage<FMT, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * kKB);
+        const Stage<FMT, BN> &S = stages[(s - st0) & 1];
+#pragma unroll 1
+        for (int blk = 0; blk < kKB; blk++) {
+            long a[2];
+            float4 xsr[2];
+            int4 sxr[2];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = min(m_o + r, M - 1);
-            xsr[r] = xs[(size_t)m * G + g];
-            sxr[r] = sx[(size_t)m * G + g];
-            fsx[r] = (float)sxr[r];
-        }
+            for (int i = 0; i < 2; i++) {
+                const int row = wm * 32 + 16 * i;
+                a[i] = *(const long *)(S.a + (row + r16) * kARow + blk * 32 + c4 * 8);
+                xsr[i] = *(const float4 *)&S.xs[blk][row + 4 * c4];
+                sxr[i] = *(const int4 *)&S.sx[blk][row + 4 * c4];
+            }
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const size_t idx = nidx[j] + g;
-            const v4i z = {0, 0, 0, 0};
-            const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b_frag<FMT>(P, idx, c4), z, 0, 0, 0);
-            if (FMT == SLLM_Q8_0) {
-                const float ws = f16_lut(P.d[idx]);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float cmb = ws * xsr[r];
-                    const float term = cmb * (float)d[r];
-                    acc[j][r] = acc[j][r] + term;
+            for (int j = 0; j < 2; j++) {
+                const int col = wn * 32 + 16 * j + r16;
+                const long b = b_frag<FMT, BN>(S, col, blk, c4);
+                const float wd = (FMT == SLLM_Q8_0) ? f16_lut(S.d[blk][col]) : f16_exact(S.d[blk][col]);
+                float wmn = 0.0f, wdh = 0.0f;
+                long bh = 0;
+                if (FMT == SLLM_Q4_1 || DUAL) wmn = f16_exact(S.m[(FMT == SLLM_Q4_1 || DUAL) ? blk : 0][col]);
+                if (DUAL) {
+                    wdh = f16_exact(S.dh[DUAL ? blk : 0][col]);
+                    bh = bits_frag(S.hb[DUAL ? blk : 0][col], c4);
                 }
-            } else if (FMT == SLLM_Q4_0) {
-                const float ws = f16_exact(P.d[idx]);
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float cmb = ws * xsr[r];
-                    const float term = cmb * (float)(d[r] - 8 * sxr[r]);
-                    acc[j][r] = acc[j][r] + term;
-                }
-            } else {
-                const float wd = f16_exact(P.d[idx]), wm = f16_exact(P.m[idx]);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float t1 = (float)d[r] * wd;
-                    const float t2 = fsx[r] * wm;
-                    float tt = t1 + t2;
-                    tt = tt * xsr[r];
-                    acc[j][r] = acc[j][r] + tt;
-                }
-                if (FMT == SLLM_Q5K1) {
-                    const v4i h = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bits_frag(P.qh[idx], c4), z, 0, 0, 0);
-                    const float wdh = f16_exact(P.dh[idx]);
+                for (int i = 0; i < 2; i++) {
+                    const v4i z = {0, 0, 0, 0};
+                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, z, 0, 0, 0);
+                    const float xv[4] = {xsr[i].x, xsr[i].y, xsr[i].z, xsr[i].w};
+                    const int sv[4] = {sxr[i].x, sxr[i].y, sxr[i].z, sxr[i].w};
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
-                        const float h1 = (float)h[r] * wdh;
-                        const float h2 = fsx[r] * 0.0f;
-                        float hh = h1 + h2;
-                        hh = hh * xsr[r];
-                        acc2[j][r] = acc2[j][r] + hh;
+                        if (FMT == SLLM_Q8_0) {
+                            // q8q8.go:193-195 + vnni_amd64.s:70-73
+                            const float cmb = wd * xv[r];
+                            const float term = cmb * (float)d[r];
+                            acc[i][j][r] = acc[i][j][r] + term;
+                        } else if (FMT == SLLM_Q4_0) {
+                            // q4q8.go:37-43
+                            const float cmb = wd * xv[r];
+                            const float term = cmb * (float)(d[r] - 8 * sv[r]);
+                            acc[i][j][r] = acc[i][j][r] + term;
+                        } else {
+                            // q41q8_row_amd64.s:65-71
+                            const float t1 = (float)d[r] * wd;
+                            const float t2 = (float)sv[r] * wmn;
+                            float tt = t1 + t2;
+                            tt = tt * xv[r];
+                            acc[i][j][r] = acc[i][j][r] + tt;
+                        }
+                    }
+                    if (DUAL) {
+                        const v4i h = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bh, z, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float h1 = (float)h[r] * wdh;
+                            const float h2 = (float)sv[r] * 0.0f;
+                            float hh = h1 + h2;
+                            hh = hh * xv[r];
+                            acc2[DUAL ? i : 0][DUAL ? j : 0][r] = acc2[DUAL ? i : 0][DUAL ? j : 0][r] + hh;
+                        }
                     }
                 }
             }
         }
+        if (s + 1 < st1) store_stage<FMT, BN, T>(f, stages[(s + 1 - st0) & 1]);
+        __syncthreads();
     }
+
+    float *o = out + (size_t)sp * M * N;  // splits > 1: partial tile of split sp
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int n = nt * kBN + 16 * j + r16;
+    for (int i = 0; i < 2; i++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int m = m_o + r;
-            if (m < M && n < N) dst[(size_t)m * N + n] = (FMT == SLLM_Q5K1) ? acc[j][r] + acc2[j][r] : acc[j][r];
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * 32 + 16 * j + r16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * 32 + 16 * i + 4 * c4 + r;
+                if (m < M && n < N) {
+                    float v = acc[i][j][r];
+                    if (DUAL) v = v + acc2[DUAL ? i : 0][DUAL ? j : 0][r];
+                    o[(size_t)m * N + n] = v;
+                }
+            }
         }
     }
 }
 
+// dst = part[0] + part[1] + ... + part[S-1], in split order.
+__global__ void reduce_splits_kernel(const float *__restrict__ part, float *__restrict__ dst, size_t n, int S) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int s = 1; s < S; s++) v = v + part[(size_t)s * n + i];
+        dst[i] = v;
+    }
+}
+
+struct GemmPlan {
+    int wn, splits, sps, mtiles, ntiles;
+};
+
+GemmPlan plan_gemm(int M, int N, int G) {
+    const int cus = 256;
+    GemmPlan p{};
+    p.mtiles = (M + kBM - 1) / kBM;
+    auto tiles = [&](int wn) { return (int64_t)p.mtiles * ((N + 32 * wn - 1) / (32 * wn)); };
+    p.wn = tiles(4) >= 2 * cus ? 4 : (tiles(2) >= cus ? 2 : 1);
+    p.ntiles = (N + 32 * p.wn - 1) / (32 * p.wn);
+    const int nst = G / kKB;
+    int S = 1;
+    while ((int64_t)p.mtiles * p.ntiles * S < 2 * cus && nst / (S * 2) >= 4) S *= 2;
+    p.splits = S;
+    p.sps = (nst + S - 1) / S;
+    return p;
+}
+
+template <int FMT, int WN>
+sllm_status launch_wn(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
+                      int N, int G, const GemmPlan &p, hipStream_t s) {
+    const int total = p.mtiles * p.ntiles * p.splits;
+    const int grid = ((total + 7) / 8) * 8;
+    const size_t lds = 2 * sizeof(Stage<FMT, 32 * WN>);
+    hipLaunchKernelGGL((gemm_kernel<FMT, WN>), dim3(grid), dim3(128 * WN), lds, s, P, xq, xsp, sxp, out, M, N, G,
+                       p.mtiles, p.ntiles, p.splits, p.sps);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+template <int FMT>
+sllm_status launch_fmt(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
+                       int N, int G, const GemmPlan &p, hipStream_t s) {
+    switch (p.wn) {
+    case 4: return launch_wn<FMT, 4>(P, xq, xsp, sxp, out, M, N, G, p, s);
+    case 2: return launch_wn<FMT, 2>(P, xq, xsp, sxp, out, M, N, G, p, s);
+    default: return launch_wn<FMT, 1>(P, xq, xsp, sxp, out, M, N, G, p, s);
+    }
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
 }  // namespace
+
+bool gemm_supported(int fmt, int G) {
+    return fmt != SLLM_Q5_0 && G % kKB == 0;
+}
 
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M) {
     (void)fmt;
-    (void)N;
-    const size_t q = ((size_t)M * G * 32 + 255) & ~(size_t)255;
-    const size_t s = ((size_t)M * G * 4 + 255) & ~(size_t)255;
-    return q + 2 * s;
+    const GemmPlan p = plan_gemm(M, N, G);
+    const size_t parts = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+    return align256((size_t)M * G * 32) + 2 * align256((size_t)M * G * 4) + align256(parts);
 }
 
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M, void *ws,
                         size_t ws_bytes, hipStream_t s) {
     if (ws_bytes < gemm_workspace_bytes(fmt, N, G, M)) return set_error(SLLM_ERR_ARG, "gemm: workspace too small");
+    if (!gemm_supported(fmt, G)) return set_error(SLLM_ERR_SHAPE, "gemm: format or cols not supported");
     int8_t *xq = (int8_t *)ws;
-    const size_t q = ((size_t)M * G * 32 + 255) & ~(size_t)255;
-    const size_t sb = ((size_t)M * G * 4 + 255) & ~(size_t)255;
+    const size_t q = align256((size_t)M * G * 32), sb = align256((size_t)M * G * 4);
     float *xsp = (float *)((char *)ws + q);
     int *sxp = (int *)((char *)ws + q + sb);
+    float *part = (float *)((char *)ws + q + 2 * sb);
     sllm_status st = launch_quantize_act(x, M, G, xq, xsp, sxp, s);
     if (st != SLLM_OK) return st;
-    const int mtiles = (M + kBM - 1) / kBM, ntiles = (N + kBN - 1) / kBN;
-    const int total = mtiles * ntiles;
-    const int grid = ((total + 7) / 8) * 8;
+    const GemmPlan p = plan_gemm(M, N, G);
+    float *out = p.splits > 1 ? part : dst;
     switch (fmt) {
-    case SLLM_Q8_0: hipLaunchKernelGGL(gemm_kernel<SLLM_Q8_0>, dim3(grid), dim3(256), 0, s, P, xq, xsp, sxp, dst, M, N, G, mtiles, ntiles); break;
-    case SLLM_Q4_0: hipLaunchKernelGGL(gemm_kernel<SLLM_Q4_0>, dim3(grid), dim3(256), 0, s, P, xq, xsp, sxp, dst, M, N, G, mtiles, ntiles); break;
-    case SLLM_Q4_1: hipLaunchKernelGGL(gemm_kernel<SLLM_Q4_1>, dim3(grid), dim3(256), 0, s, P, xq, xsp, sxp, dst, M, N, G, mtiles, ntiles); break;
-    case SLLM_Q5K1: hipLaunchKernelGGL(gemm_kernel<SLLM_Q5K1>, dim3(grid), dim3(256), 0, s, P, xq, xsp, sxp, dst, M, N, G, mtiles, ntiles); break;
+    case SLLM_Q8_0: st = launch_fmt<SLLM_Q8_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+    case SLLM_Q4_0: st = launch_fmt<SLLM_Q4_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+    case SLLM_Q4_1: st = launch_fmt<SLLM_Q4_1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+    case SLLM_Q5K1: st = launch_fmt<SLLM_Q5K1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
     default: return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
     }
+    if (st != SLLM_OK || p.splits == 1) return st;
+    const size_t n = (size_t)M * N;
+    int grid = (int)((n + 255) / 256);
+    if (grid > 4096) grid = 4096;
+    hipLaunchKernelGGL(reduce_splits_kernel, dim3(grid), dim3(256), 0, s, part, dst, n, p.splits);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

@@ -92,6 +92,7 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         void *ws, size_t ws_bytes, hipStream_t s);
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M);
+bool gemm_supported(int fmt, int G);  // Q5_0 and K not a multiple of 128 stay on the GEMV
 sllm_status launch_quantize_act(const float *x, int rows, int G, int8_t *xq, float *xs, int32_t *sx,
                                 hipStream_t s);
 sllm_status launch_block_dots(int fmt, const Planes &P, const float *x, int N, int G, int M,
