@@ -45,6 +45,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--decode-tokens", type=int, default=20)
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant GEMV and a 256 MiB copy (for rocprofv3 --pmc runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -64,6 +66,8 @@ def main() -> int:
     sp = stream.cuda_stream
 
     H, F = 4096, 14336
+    if args.traffic_probe:
+        return traffic_probe(sq, synth, torch, stream, args.layers)
     print(f"[bench] building {args.layers} layer copies of C3 weights", file=sys.stderr, flush=True)
     gate_raw = synth.q4k_blocks(100, F, H)
     up_raw = synth.q4k_blocks(101, F, H)
@@ -134,6 +138,11 @@ def main() -> int:
     if not args.no_decode:
         extra.update(decode_tok_s(sq, synth, torch, stream, args.decode_tokens))
 
+    tr = load_traffic()
+    traffic_bytes = tr["traffic_bytes_per_launch"] if tr else None
+    if tr:
+        extra["traffic_source"] = tr["source"]
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(layers, step_bytes)
@@ -165,13 +174,46 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic_bytes,
         },
         "cpu_baseline": cpu,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+COPY_BYTES = 256 << 20
+
+
+def traffic_probe(sq, synth, torch, stream, copies: int) -> int:
+    """Launches for the counter runs: 20 Q8_0 down GEMVs (rotating copies), then
+    5 device copies of COPY_BYTES (the calibration kernel of known traffic)."""
+    H, F = 4096, 14336
+    raw = synth.q6k_blocks(102, H, F)
+    ws = [sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, H, F) for _ in range(copies)]
+    h = torch.from_numpy(synth.normal(2, F)).cuda()
+    yd = torch.empty(H, device="cuda")
+    for i in range(20):
+        w = ws[i % len(ws)]
+        sq.matmul_dev(w, h.data_ptr(), 1, F, yd.data_ptr(), stream.cuda_stream)
+    a = torch.empty(COPY_BYTES // 4, device="cuda")
+    b = torch.empty(COPY_BYTES // 4, device="cuda")
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(f"traffic probe done: down GEMV plane bytes {ws[0].plane_bytes}, copy {COPY_BYTES} B", flush=True)
+    return 0
+
+
+def load_traffic() -> dict | None:
+    """HBM bytes per launch of the dominant kernel from the committed counter runs."""
+    path = os.path.join(ROOT, "profiles", "traffic_gemv_q8_down_c3.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
