@@ -4,17 +4,23 @@ Workload (the one the metric is quoted on): one Llama-3-8B
 layer's decode GEMVs at M = 1 token -
     gate, up : Q4_K 14336 x 4096, remapped at load to Q4_1 (20 B / 32 weights)
     down     : Q6_K 4096 x 14336, requantized at load to Q8_0 (34 B / 32)
-A step is the three GEMVs over one layer's weights; steps rotate over enough
-layer copies (> 1 GiB) that no step finds its weights in the 256 MB MALL.
-Inputs are synthetic, already resident in HBM; the remap runs once at load.
+A step is those three matmuls over one layer's weights: gate and up share
+their input and run as one launch (sllm_matmul_multi_dev), down as another.
+Steps rotate over enough layer copies (> 1 GiB) that no step finds its
+weights in the 256 MB MALL. Inputs are synthetic, already resident in HBM;
+the remaps run once at load.
 
-value        = algorithmic bytes per step x steps / elapsed   (GB/s, whole job)
-roofline     = dominant kernel (the Q8_0 down GEMV): algorithmic bytes per launch
-               / its mean duration (HIP events around back-to-back launches)
+value        = algorithmic bytes per step x steps / elapsed   (GB/s, whole job);
+               per GEMV: plane bytes + 4 K (fp32 x) + 4 N (fp32 out)
+roofline     = dominant kernel (the fused gate+up Q4_1 GEMV, 54 % of the step's
+               bytes): its algorithmic bytes per launch / its mean duration (HIP
+               events around back-to-back launches on the launch stream)
 cpu_baseline = the reference's CPU kernels restated with AVX2/AVX-VNNI intrinsics
                and its worker pool (oracle/refcpu_simd.c), on a bounded sample
-extra        = decode tok/s over all 225 GEMVs of a 32-layer Q4_K_M 8B-shaped
-               model + Q6_K head (weights only; attention etc. not included)
+extra        = per-kernel times; every other BASELINE config's kernels (C1, C2,
+               C4 GEMV and GEMM); decode tok/s over all linears of a 32-layer
+               Q4_K_M 8B-shaped model + Q6_K head (weights only; attention etc.
+               are not part of this path)
 """
 from __future__ import annotations
 
@@ -28,12 +34,16 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "scriptling-llm-lib_amd"))
 
 HBM_PEAK_GBS = 8000.0
+INT8_MFMA_PEAK_TOPS = 5000.0
 METRIC = "quant GEMV GB/s (% of 8 TB/s HBM); Q4_K_M 8B-shape decode tok/s"
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4_1_gate_up_c3.json")
+ROTATE_BYTES = 1 << 30  # weight copies per timed kernel: > 4x the 256 MB MALL
 
 
-def algo_bytes(w, m_rows: int = 1) -> int:
-    """Weight plane bytes + fp32 activations in + fp32 outputs out."""
-    return w.plane_bytes + 4 * w.cols * m_rows + 4 * w.rows * m_rows
+def algo_bytes(ws, m_rows: int = 1) -> int:
+    """Weight plane bytes + fp32 activations in (once per launch) + fp32 outputs."""
+    ws = ws if isinstance(ws, (list, tuple)) else [ws]
+    return sum(w.plane_bytes + 4 * w.rows * m_rows for w in ws) + 4 * ws[0].cols * m_rows
 
 
 def main() -> int:
@@ -44,6 +54,7 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=8, help="layer copies rotated over (>1 GiB)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1/C2/C4 kernel table")
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant GEMV and a 256 MiB copy (for rocprofv3 --pmc runs)")
@@ -54,7 +65,6 @@ def main() -> int:
               file=sys.stderr)
         return 2
 
-    import numpy as np
     import torch
 
     import sllm_qmm as sq
@@ -85,11 +95,21 @@ def main() -> int:
     yd = torch.empty(H, device="cuda")
     step_bytes = algo_bytes(g0) + algo_bytes(u0) + algo_bytes(d0)
 
-    def step(i):
-        g, u, d = layers[i % len(layers)]
-        sq.matmul_dev(g, x.data_ptr(), 1, H, yg.data_ptr(), sp)
-        sq.matmul_dev(u, x.data_ptr(), 1, H, yu.data_ptr(), sp)
+    def gate_up(i):
+        g, u, _ = layers[i % len(layers)]
+        sq.matmul_multi_dev([g, u], x.data_ptr(), 1, H, [yg.data_ptr(), yu.data_ptr()], sp)
+
+    def down(i):
+        d = layers[i % len(layers)][2]
         sq.matmul_dev(d, h.data_ptr(), 1, F, yd.data_ptr(), sp)
+
+    def gate_only(i):
+        g = layers[i % len(layers)][0]
+        sq.matmul_dev(g, x.data_ptr(), 1, H, yg.data_ptr(), sp)
+
+    def step(i):
+        gate_up(i)
+        down(i)
 
     for i in range(args.warmup):
         step(i)
@@ -105,36 +125,25 @@ def main() -> int:
     ms_per_step = elapsed_ms / args.steps
     value = step_bytes * args.steps / (elapsed_ms * 1e-3) / 1e9
 
-    # Per-kernel mean duration: back-to-back launches of one GEMV (rotating over
-    # the layer copies) between two events on the launch stream. Consecutive
-    # launches on one stream run with no measurable gap, so this is the kernel
-    # time that rocprofv3 --kernel-trace reports for the same launches.
-    def time_kernel(widx, xin, yout, n):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        for i in range(8):
-            w = layers[i % len(layers)][widx]
-            sq.matmul_dev(w, xin.data_ptr(), 1, w.cols, yout.data_ptr(), sp)
-        a.record(stream)
-        for i in range(n):
-            w = layers[i % len(layers)][widx]
-            sq.matmul_dev(w, xin.data_ptr(), 1, w.cols, yout.data_ptr(), sp)
-        b.record(stream)
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / n * 1e3
-
-    down_us = time_kernel(2, h, yd, args.steps)
-    down_bytes = algo_bytes(d0)
-    achieved = down_bytes / (down_us * 1e-6) / 1e9
-    gate_us = time_kernel(0, x, yg, args.steps)
+    gu_us = time_launches(torch, stream, gate_up, args.steps)
+    gu_bytes = algo_bytes([g0, u0])
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    down_us = time_launches(torch, stream, down, args.steps)
+    gate_us = time_launches(torch, stream, gate_only, args.steps)
 
     extra = {
-        "gate_q4_1_gemv_us": round(gate_us, 3),
-        "gate_q4_1_gemv_GBps": round(algo_bytes(g0) / (gate_us * 1e-6) / 1e9, 1),
+        "gate_up_fused_q4_1_gemv_us": round(gu_us, 3),
+        "gate_up_fused_bytes": gu_bytes,
         "down_q8_0_gemv_us": round(down_us, 3),
+        "down_q8_0_gemv_GBps": round(algo_bytes(d0) / (down_us * 1e-6) / 1e9, 1),
+        "gate_q4_1_gemv_alone_us": round(gate_us, 3),
+        "gate_q4_1_gemv_alone_GBps": round(algo_bytes(g0) / (gate_us * 1e-6) / 1e9, 1),
         "kernel_info": sq.kernel_info(),
     }
+    del layers
 
+    if not args.no_configs:
+        extra["configs"] = config_table(sq, synth, torch, stream)
     if not args.no_decode:
         extra.update(decode_tok_s(sq, synth, torch, stream, args.decode_tokens))
 
@@ -145,7 +154,7 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(layers, step_bytes)
+        cpu = cpu_baseline(sq, synth, gate_raw, up_raw, down_raw, args.layers, step_bytes)
 
     line = {
         "metric": METRIC,
@@ -161,15 +170,15 @@ def main() -> int:
         "dtype": "int8",
         "data": "synthetic",
         "config": {
-            "workload": "C3: Llama-3-8B Q4_K_M layer decode GEMVs, M=1: Q4_K gate+up 14336x4096 -> Q4_1, "
-                        "Q6_K down 4096x14336 -> Q8_0",
+            "workload": "C3: Llama-3-8B Q4_K_M layer decode GEMVs, M=1: Q4_K gate+up 14336x4096 -> Q4_1 "
+                        "(one fused launch), Q6_K down 4096x14336 -> Q8_0",
             "bytes_per_step": step_bytes,
             "rotating_layer_copies": args.layers,
             "parallelism": "single GPU",
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gemv_kernel<Q8_0> (Q6_K->Q8_0 down 4096x14336)",
+            "kernel": "gemv_kernel<Q4_1>, gate+up fused (2 x Q4_K->Q4_1 14336x4096, one launch)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
@@ -183,42 +192,133 @@ def main() -> int:
     return 0
 
 
+def time_launches(torch, stream, launch, n: int, warm: int = 8) -> float:
+    """Mean duration (us) of `launch(i)` over n back-to-back calls between two HIP
+    events on the launch stream. Consecutive launches on one stream run with no
+    measurable gap, so this is the kernel time rocprofv3 --kernel-trace reports
+    for the same launches."""
+    for i in range(warm):
+        launch(i)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for i in range(n):
+        launch(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n * 1e3
+
+
+def config_table(sq, synth, torch, stream) -> dict:
+    """The kernels of BASELINE configs C1, C2, C4 (and C3 at prefill sizes).
+
+    Each entry rotates over copies of its weight totalling >= 1 GiB (at most
+    512 copies, so C1's 0.9 MB weight can stay in the MALL: C1 is launch-bound
+    at any rate). GEMV lines give GB/s of algorithmic bytes; GEMM lines (M >=
+    64) also give int8 TOPS (2 M N K per call) against the 5.0 POPS dense int8
+    peak. Q5_K rows stream 26 B / 32 weights (the two Q4_1 halves of
+    convertQ5KToTwoQ41 without the high half's zero mins and 4-bit codes)."""
+    import numpy as np
+    H, F, KV = 4096, 14336, 1024
+    sp = stream.cuda_stream
+    print("[bench] config table (C1, C2, C4 and C3 prefill)", file=sys.stderr, flush=True)
+
+    def copies(make_one):
+        w0 = make_one()
+        n = int(min(512, max(2, -(-ROTATE_BYTES // w0.plane_bytes))))
+        q = sq.QuantWeight(w0.qtype, w0.export(), w0.groups, w0.rows, w0.cols)
+        return [w0] + [sq.DeviceWeight.from_quant(q) for _ in range(n - 1)]
+
+    def run(ws, M, reps):
+        K, N = ws[0].cols, ws[0].rows
+        xin = torch.from_numpy(synth.normal(7, M * K)).cuda()
+        out = torch.empty(M * N, device="cuda")
+        us = time_launches(torch, stream, lambda i: sq.matmul_dev(ws[i % len(ws)], xin.data_ptr(), M, K,
+                                                                   out.data_ptr(), sp), reps)
+        nbytes = algo_bytes(ws[0], M)
+        r = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+             "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if M >= 64:
+            tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
+            r.update({"TOPS": round(tops, 1), "frac_int8_mfma": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                      "path": "gemm" if ws[0].qtype != "q5" else "gemv (Q5_0 has fp32 activations)"})
+        return r
+
+    def q_from_f32(qtype, seed, N, K):
+        wf = synth.normal(seed, N * K, 0.02).reshape(N, K)
+        raw = {"q4": synth.quantize_q4_0, "q4_1": synth.quantize_q4_1, "q5": synth.quantize_q5_0}[qtype](wf)
+        return lambda: sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+
+    table = {}
+    c1 = copies(lambda: sq.quantize_q8_rows_f32(synth.normal(0, 1536 * 576, 0.02), 1536, 576))
+    table["C1 q8 1536x576 M=1"] = run(c1, 1, 400)
+    del c1
+    for qtype in ("q4", "q4_1"):
+        for N, K in ((8192, 2048), (2048, 8192)):
+            ws = copies(q_from_f32(qtype, 10 + N // 1024, N, K))
+            table[f"C2 {qtype} {N}x{K} M=1"] = run(ws, 1, 200)
+            del ws
+    for N in (H, KV, F):
+        ws = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q5_K, synth.q5k_blocks(20 + N // 1024, N, H), N, H))
+        for M in (1, 64, 512):
+            table[f"C4 q5k1 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else 20)
+        del ws
+        ws = copies(q_from_f32("q5", 30 + N // 1024, N, H))
+        for M in (1, 64, 512):
+            table[f"C4 q5 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else (20 if M == 64 else 4))
+        del ws
+    g = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(100, F, H), F, H))
+    for M in (64, 512):
+        table[f"C3 q4_1 gate {F}x{H} M={M}"] = run(g, M, 20)
+    del g
+    d = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q6_K, synth.q6k_blocks(102, H, F), H, F))
+    for M in (64, 512):
+        table[f"C3 q8 down {H}x{F} M={M}"] = run(d, M, 20)
+    del d
+    torch.cuda.empty_cache()
+    return table
+
+
 COPY_BYTES = 256 << 20
 
 
 def traffic_probe(sq, synth, torch, stream, copies: int) -> int:
-    """Launches for the counter runs: 20 Q8_0 down GEMVs (rotating copies), then
-    5 device copies of COPY_BYTES (the calibration kernel of known traffic)."""
+    """Launches for the counter runs: 20 fused gate+up GEMVs (rotating copies),
+    then 5 device copies of COPY_BYTES (the calibration kernel of known traffic)."""
     H, F = 4096, 14336
-    raw = synth.q6k_blocks(102, H, F)
-    ws = [sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, H, F) for _ in range(copies)]
-    h = torch.from_numpy(synth.normal(2, F)).cuda()
-    yd = torch.empty(H, device="cuda")
+    gr, ur = synth.q4k_blocks(100, F, H), synth.q4k_blocks(101, F, H)
+    pairs = [(sq.load_weight_f32_direct(synth.GGML_Q4_K, gr, F, H),
+              sq.load_weight_f32_direct(synth.GGML_Q4_K, ur, F, H)) for _ in range(copies)]
+    x = torch.from_numpy(synth.normal(1, H)).cuda()
+    yg = torch.empty(F, device="cuda")
+    yu = torch.empty(F, device="cuda")
     for i in range(20):
-        w = ws[i % len(ws)]
-        sq.matmul_dev(w, h.data_ptr(), 1, F, yd.data_ptr(), stream.cuda_stream)
+        g, u = pairs[i % len(pairs)]
+        sq.matmul_multi_dev([g, u], x.data_ptr(), 1, H, [yg.data_ptr(), yu.data_ptr()], stream.cuda_stream)
     a = torch.empty(COPY_BYTES // 4, device="cuda")
     b = torch.empty(COPY_BYTES // 4, device="cuda")
     for _ in range(5):
         b.copy_(a)
     torch.cuda.synchronize()
-    print(f"traffic probe done: down GEMV plane bytes {ws[0].plane_bytes}, copy {COPY_BYTES} B", flush=True)
+    print(f"traffic probe done: gate+up algorithmic bytes {algo_bytes(list(pairs[0]))}, copy {COPY_BYTES} B",
+          flush=True)
     return 0
 
 
 def load_traffic() -> dict | None:
     """HBM bytes per launch of the dominant kernel from the committed counter runs."""
-    path = os.path.join(ROOT, "profiles", "traffic_gemv_q8_down_c3.json")
     try:
-        with open(path) as f:
+        with open(TRAFFIC_JSON) as f:
             return json.load(f)
     except (OSError, ValueError):
         return None
 
 
 def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
-    """All linears of one decode token of a 32-layer Q4_K_M Llama-3-8B shape + Q6_K head."""
-    import numpy as np
+    """All linears of one decode token of a 32-layer Q4_K_M Llama-3-8B shape + Q6_K head.
+
+    Per layer: q/k/v (one launch: they share their input), o, gate/up (one
+    launch), down; then the head: 32 x 4 + 1 = 129 launches per token."""
     H, F, KV, V, L = 4096, 14336, 1024, 128256, 32
     print("[bench] building the 32-layer decode weight set", file=sys.stderr, flush=True)
     q4k_hh = synth.q4k_blocks(200, H, H)
@@ -236,15 +336,19 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     tok_bytes = sum(w.plane_bytes for ws in layer_ws for w in ws) + head.plane_bytes
     xh = torch.from_numpy(synth.normal(3, H)).cuda()
     xf = torch.from_numpy(synth.normal(4, F)).cuda()
-    out = torch.empty(V, device="cuda")
+    q, k, v = (torch.empty(n, device="cuda") for n in (H, KV, KV))
+    o, gt, up, dn = (torch.empty(n, device="cuda") for n in (H, F, F, H))
+    logits = torch.empty(V, device="cuda")
     sp = stream.cuda_stream
+    P = lambda t: t.data_ptr()
 
     def token():
-        for ws in layer_ws:
-            for w in ws:
-                src = xf if w.cols == F else xh
-                sq.matmul_dev(w, src.data_ptr(), 1, w.cols, out.data_ptr(), sp)
-        sq.matmul_dev(head, xh.data_ptr(), 1, H, out.data_ptr(), sp)
+        for wq, wk, wv, wo, wg, wu, wd in layer_ws:
+            sq.matmul_multi_dev([wq, wk, wv], P(xh), 1, H, [P(q), P(k), P(v)], sp)
+            sq.matmul_dev(wo, P(xh), 1, H, P(o), sp)
+            sq.matmul_multi_dev([wg, wu], P(xh), 1, H, [P(gt), P(up)], sp)
+            sq.matmul_dev(wd, P(xf), 1, F, P(dn), sp)
+        sq.matmul_dev(head, P(xh), 1, H, P(logits), sp)
 
     for _ in range(3):
         token()
@@ -258,39 +362,46 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / tokens
     del layer_ws, head
+    torch.cuda.empty_cache()
     return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
             "decode_weight_bytes_per_token": tok_bytes,
             "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
-            "decode_note": "225 GEMV launches per token (32 layers x 7 + head); attention, norms not included"}
+            "decode_note": "129 launches per token (32 layers x [qkv, o, gate+up, down] + head); "
+                           "attention, norms, SwiGLU not included"}
 
 
-def cpu_baseline(layers, step_bytes: int, budget_s: float = 12.0) -> dict:
+def cpu_baseline(sq, synth, gate_raw, up_raw, down_raw, copies: int, step_bytes: int,
+                 budget_s: float = 12.0) -> dict:
     """Restated reference CPU path (AVX2/AVX-VNNI kernels, parallel.go pool) on C3 steps.
 
-    Steps rotate over the same layer copies as the GPU run (> 1 GiB), so the
+    The weights are the same remapped bytes the GPU streams (exported from the
+    device planes). Steps rotate over `copies` layer copies (> 1 GiB), so the
     host's caches do not hold the weights either; runs for ~budget_s seconds.
     """
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import ctypes as C
     import numpy as np
     import oracle  # the cpu_baseline leg is the one part of bench.py allowed to use oracle/
-    from sllm_qmm import synth
 
+    H, F = 4096, 14336
     B = oracle.baseline()
     workers = B.bl_workers()
-    g0 = layers[0][0]
-    x = synth.normal(1, g0.cols).reshape(1, -1)
-    hx = synth.normal(2, layers[0][2].cols).reshape(1, -1)
-    host = [tuple(w.export() for w in ly) for ly in layers]
-    yg = np.empty(g0.rows, np.float32)
-    yd = np.empty(layers[0][2].rows, np.float32)
+    one = [sq.load_weight_f32_direct(synth.GGML_Q4_K, gate_raw, F, H),
+           sq.load_weight_f32_direct(synth.GGML_Q4_K, up_raw, F, H),
+           sq.load_weight_f32_direct(synth.GGML_Q6_K, down_raw, H, F)]
+    base = [w.export() for w in one]
+    host = [tuple(b.copy() for b in base) for _ in range(copies)]
+    x = synth.normal(1, H).reshape(1, -1)
+    hx = synth.normal(2, F).reshape(1, -1)
+    yg = np.empty(F, np.float32)
+    yd = np.empty(H, np.float32)
     P = lambda a: C.c_void_p(a.ctypes.data)
 
     def step(i):
-        (gr, ur, dr), (g, u, d) = host[i % len(host)], layers[i % len(layers)]
-        B.bl_matmul(b"q4_1", P(gr), g.rows, g.cols, P(x), 1, P(yg))
-        B.bl_matmul(b"q4_1", P(ur), u.rows, u.cols, P(x), 1, P(yg))
-        B.bl_matmul(b"q8", P(dr), d.rows, d.cols, P(hx), 1, P(yd))
+        gr, ur, dr = host[i % len(host)]
+        B.bl_matmul(b"q4_1", P(gr), F, H, P(x), 1, P(yg))
+        B.bl_matmul(b"q4_1", P(ur), F, H, P(x), 1, P(yg))
+        B.bl_matmul(b"q8", P(dr), H, F, P(hx), 1, P(yd))
 
     for i in range(len(host)):
         step(i)
@@ -300,13 +411,13 @@ def cpu_baseline(layers, step_bytes: int, budget_s: float = 12.0) -> dict:
         step(n)
         n += 1
     sec = (time.time() - t0) / n
+    isa = "VNNI" if B.bl_has_vnni() else "AVX2"
     return {
         "value": round(step_bytes / sec / 1e9, 2),
         "unit": "GB/s",
         "cores": workers,
         "kind": "port",
-        "sample": f"{n} C3 steps rotating over {len(host)} layer copies (gate+up Q4_1 "
-                  f"{'VNNI' if B.bl_has_vnni() else 'AVX2'}, down Q8_0 {'VNNI' if B.bl_has_vnni() else 'AVX2'}), "
+        "sample": f"{n} C3 steps rotating over {len(host)} layer copies (gate+up Q4_1 {isa}, down Q8_0 {isa}), "
                   f"{sec * 1e3:.2f} ms/step over {n * sec:.1f} s; {workers} worker threads (parallel.go rule)",
     }
 

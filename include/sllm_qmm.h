@@ -131,6 +131,23 @@ sllm_status sllm_matmul_row_quant_into_f32(const sllm_weight *w, const float *no
 sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x_dev, int x_rows, int x_cols,
                             float *dst_dev, void *stream);
 
+/*
+ * Several weights applied to the same activation rows: the consecutive
+ * modelMatmulIntoF32 calls of forwardBlock that share one input (q, k, v on
+ * b.normed, model_f32.go:391-396; gate, up on b.ffnNormed, model_f32.go:479-482).
+ * Equivalent to count calls of sllm_matmul_quant_into_f32 (dst[i] receives
+ * x_rows x Rows(ws[i]) floats, bit-identical to the single call's result),
+ * but decode GEMVs of weights with the same QType share one launch (up to
+ * four weights each) and x is uploaded once. Every ws[i] must have
+ * Cols == x_cols.
+ */
+sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int count, const float *x,
+                                             int x_rows, int x_cols, float *const *dst);
+
+/* Device-resident form of sllm_matmul_multi_quant_into_f32 (see sllm_matmul_dev). */
+sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x_dev, int x_rows,
+                                  int x_cols, float *const *dst_dev, void *stream);
+
 /* argmaxF32 (float32_ops.go:812-822) over n device floats; result to host. */
 sllm_status sllm_argmax_dev(const float *v_dev, int n, int *out, void *stream);
 

@@ -461,6 +461,82 @@ sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int
     return st;
 }
 
+sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x, int x_rows, int x_cols,
+                                  float *const *dst, void *stream) {
+    if (!ws || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (count <= 0) return set_error(SLLM_ERR_ARG, "count must be positive");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !dst[i]) return set_error(SLLM_ERR_ARG, "null weight or dst");
+        if (ws[i]->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match a weight's Cols");
+    }
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    // weights that take the GEMV: grouped by format, up to kMaxSegs per launch
+    std::vector<char> done((size_t)count, 0);
+    for (int i = 0; i < count; i++) {
+        if (done[(size_t)i]) continue;
+        const sllm_weight *w = ws[i];
+        if (x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups)) {
+            done[(size_t)i] = 1;
+            if ((st = sllm_matmul_dev(w, x, x_rows, x_cols, dst[i], stream)) != SLLM_OK) return st;
+            continue;
+        }
+        Planes P[kMaxSegs];
+        float *D[kMaxSegs];
+        int N[kMaxSegs];
+        int n = 0;
+        for (int j = i; j < count && n < kMaxSegs; j++) {
+            if (done[(size_t)j] || ws[j]->fmt != w->fmt) continue;
+            P[n] = as_const(ws[j]->planes);
+            D[n] = dst[j];
+            N[n] = ws[j]->rows;
+            n++;
+            done[(size_t)j] = 1;
+        }
+        if ((st = launch_gemv_multi(w->fmt, P, D, N, n, x, w->groups, x_rows, s)) != SLLM_OK) return st;
+    }
+    return SLLM_OK;
+}
+
+sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int count, const float *x, int x_rows,
+                                             int x_cols, float *const *dst) {
+    if (!ws || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (count <= 0) return set_error(SLLM_ERR_ARG, "count must be positive");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !dst[i]) return set_error(SLLM_ERR_ARG, "null weight or dst");
+        if (ws[i]->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match a weight's Cols");
+    }
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    // staging: x, then each output, 256-byte aligned
+    const size_t xb = (size_t)x_rows * x_cols * sizeof(float);
+    std::vector<size_t> off((size_t)count);
+    size_t total = (xb + 255) & ~(size_t)255;
+    for (int i = 0; i < count; i++) {
+        off[(size_t)i] = total;
+        total += ((size_t)x_rows * ws[i]->rows * sizeof(float) + 255) & ~(size_t)255;
+    }
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, total)) != SLLM_OK) return st;
+    std::vector<float *> dd((size_t)count);
+    for (int i = 0; i < count; i++) dd[(size_t)i] = (float *)((char *)c->buf + off[(size_t)i]);
+    hipError_t e = hipMemcpyAsync(c->buf, x, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = sllm_matmul_multi_dev(ws, count, (const float *)c->buf, x_rows, x_cols, dd.data(), c->stream);
+        for (int i = 0; st == SLLM_OK && e == hipSuccess && i < count; i++)
+            e = hipMemcpyAsync(dst[i], dd[(size_t)i], (size_t)x_rows * ws[i]->rows * sizeof(float),
+                               hipMemcpyDeviceToHost, c->stream);
+        if (st == SLLM_OK && e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "matmul transfer");
+    return st;
+}
+
 sllm_status sllm_matmul_row_quant_into_f32(const sllm_weight *w, const float *normed, float *dst) {
     if (!w) return set_error(SLLM_ERR_ARG, "null weight");
     return sllm_matmul_quant_into_f32(w, normed, 1, w->cols, dst);

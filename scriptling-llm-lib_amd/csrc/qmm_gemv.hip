@@ -235,21 +235,46 @@ __device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB
     }
 }
 
+// The weights of one launch (same format, same K, same activation rows).
+// Segment s owns the waves [wave0[s], wave0[s + 1]) of the grid; wave0[n] is
+// the grid's wave count, so the last segment also takes the spare waves.
+struct SegTable {
+    Planes P[kMaxSegs];
+    float *dst[kMaxSegs];
+    int N[kMaxSegs];
+    int wave0[kMaxSegs + 1];
+    int n;
+};
+
 // A wave's work is a stream of units: unit t is K-chunk (t % KCH) of its row
-// number (t / KCH), rows being wv, wv + TW, ... (at most RPW of them). A unit
-// is NB blocks per lane. The wave keeps D units in flight in a register ring:
-// it computes unit t, then issues the loads of unit t + D into the registers
-// it just consumed.
+// number (t / KCH), rows being wv, wv + TW, ... of its segment's weight (at
+// most RPW of them). A unit is NB blocks per lane. The wave keeps D units in
+// flight in a register ring: it computes unit t, then issues the loads of
+// unit t + D into the registers it just consumed.
 template <int FMT, int NB, int D, int MT, bool HOIST>
-__global__ void __launch_bounds__(1024) gemv_kernel(Planes P, const float *__restrict__ x,
-                                                    float *__restrict__ dst, int N, int G, int M, int KCH,
-                                                    int RPW, int tpb) {
+__global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__restrict__ x, int G, int M,
+                                                    int KCH, int RPW, int tpb) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
     const ActView A = carve_act(lds, FMT, MT, G);
     const int lane = threadIdx.x & 63;
     const int W = blockDim.x >> 6;
-    const int TW = gridDim.x * W;
-    const int wv = blockIdx.x * W + (threadIdx.x >> 6);
+    // this wave's segment (wave-uniform, so the selection stays in scalar registers)
+    const int wg = __builtin_amdgcn_readfirstlane(blockIdx.x * W + (threadIdx.x >> 6));
+    Planes P = S.P[0];
+    float *__restrict__ dst = S.dst[0];
+    int N = S.N[0], w0 = 0, w1 = S.wave0[1];
+#pragma unroll
+    for (int s = 1; s < kMaxSegs; s++) {
+        if (s < S.n && wg >= S.wave0[s]) {
+            P = S.P[s];
+            dst = S.dst[s];
+            N = S.N[s];
+            w0 = S.wave0[s];
+            w1 = S.wave0[s + 1];
+        }
+    }
+    const int TW = w1 - w0;
+    const int wv = wg - w0;
     const int U = RPW * KCH;
     constexpr int CH = 64 * NB;  // blocks per K-chunk
 
@@ -358,57 +383,57 @@ __global__ void __launch_bounds__(1024) gemv_kernel(Planes P, const float *__res
 }
 
 template <int FMT, int NB, int D, int MT>
-sllm_status launch_t(const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH, int RPW, int W,
-                     int grid, size_t lds, hipStream_t s) {
+sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
+                     size_t lds, hipStream_t s) {
     // hoisting needs room for the operands: not for Q5_0 (32 fp32 per block)
     constexpr bool kCanHoist = FMT != SLLM_Q5_0 && NB * MT <= 4;
     // lanes per activation block in the prologue: as many as the workgroup allows
     int tpb = 8;
     while (tpb > 1 && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
     if (kCanHoist && KCH == 1)
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist>), dim3(grid), dim3(W * 64), lds, s, P, x, dst, N,
-                           G, M, KCH, RPW, tpb);
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M,
+                           KCH, RPW, tpb);
     else
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false>), dim3(grid), dim3(W * 64), lds, s, P, x, dst, N, G,
-                           M, KCH, RPW, tpb);
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M, KCH,
+                           RPW, tpb);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }
 
 // D units in flight; NB * D * MT <= 8 blocks per lane.
 template <int FMT, int NB, int MT>
-sllm_status launch_d(int D, const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH, int RPW,
-                     int W, int grid, size_t lds, hipStream_t s) {
+sllm_status launch_d(int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
+                     size_t lds, hipStream_t s) {
     constexpr int DMAX = 8 / (NB * MT) >= 8 ? 8 : (8 / (NB * MT) >= 4 ? 4 : (8 / (NB * MT) >= 2 ? 2 : 1));
-    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    return launch_t<FMT, NB, 1, MT>(P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    return launch_t<FMT, NB, 1, MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
 }
 
 template <int FMT, int MT>
-sllm_status launch_nb(int NB, int D, const Planes &P, const float *x, float *dst, int N, int G, int M, int KCH,
-                      int RPW, int W, int grid, size_t lds, hipStream_t s) {
+sllm_status launch_nb(int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W,
+                      int grid, size_t lds, hipStream_t s) {
     switch (NB) {
-    case 1: return launch_d<FMT, 1, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_d<FMT, 2, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 3: return launch_d<FMT, 3, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_d<FMT, 4, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 5: return launch_d<FMT, 5, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 6: return launch_d<FMT, 6, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 7: return launch_d<FMT, 7, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 8: return launch_d<FMT, 8, MT>(D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 1: return launch_d<FMT, 1, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_d<FMT, 2, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 3: return launch_d<FMT, 3, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_d<FMT, 4, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 5: return launch_d<FMT, 5, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 6: return launch_d<FMT, 6, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 7: return launch_d<FMT, 7, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 8: return launch_d<FMT, 8, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported blocks-per-lane");
 }
 
 template <int FMT>
-sllm_status launch_mt(int MT, int NB, int D, const Planes &P, const float *x, float *dst, int N, int G, int M,
-                      int KCH, int RPW, int W, int grid, size_t lds, hipStream_t s) {
+sllm_status launch_mt(int MT, int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW,
+                      int W, int grid, size_t lds, hipStream_t s) {
     switch (MT) {
-    case 1: return launch_nb<FMT, 1>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_nb<FMT, 2>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_nb<FMT, 4>(NB, D, P, x, dst, N, G, M, KCH, RPW, W, grid, lds, s);
+    case 1: return launch_nb<FMT, 1>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_nb<FMT, 2>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_nb<FMT, 4>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported row tile");
 }
@@ -430,11 +455,17 @@ int device_cus() {
 
 }  // namespace
 
-sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
-                        hipStream_t s) {
-    if (N <= 0 || G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
+sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
+                              const float *x, int G, int M, hipStream_t s) {
+    if (nseg < 1 || nseg > kMaxSegs) return set_error(SLLM_ERR_ARG, "gemv: 1 to 4 weights per launch");
+    if (G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
+    int64_t Ntot = 0;
+    for (int i = 0; i < nseg; i++) {
+        if (N[i] <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
+        Ntot += N[i];
+    }
     const Tuning &T = tuning();
-    const int cus = device_cus();
+    const int64_t wgs = (int64_t)device_cus() * T.gemv_wg_per_cu;
     // Blocks per lane per unit. Rows of up to 8 x 64 blocks are one unit
     // (one K-chunk, issued at once); longer rows are split into K-chunks of
     // the largest lane-group count <= 8 that divides them (no partial chunks).
@@ -447,15 +478,32 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
         if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
     }
     const int KCH = (G + 64 * NB - 1) / (64 * NB);
-    int W = T.gemv_waves;
-    while (W > 4 && (int64_t)(W / 2) * cus * T.gemv_wg_per_cu >= N) W /= 2;  // small row counts: more CUs
-    // rows per wave for one pass over the device, then just enough waves for
-    // that many rows each (every wave gets RPW rows, at most W - 1 spare)
-    const int64_t slots = (int64_t)cus * T.gemv_wg_per_cu * W;
-    const int RPW = (int)((N + slots - 1) / slots);
+    // Rows per wave: the fewest that fit every segment's rows into
+    // gemv_waves waves per workgroup slot. Each segment gets just enough waves
+    // for that many rows each; the waves per workgroup are then the fewest
+    // (>= 4, for the prologue) that spread them over every workgroup slot.
+    const int64_t slots = wgs * T.gemv_waves;
+    int RPW = (int)((Ntot + slots - 1) / slots);
+    auto count_waves = [&](int rpw) {
+        int64_t w = 0;
+        for (int i = 0; i < nseg; i++) w += ((int64_t)N[i] + rpw - 1) / rpw;
+        return w;
+    };
+    while (count_waves(RPW) > slots) RPW++;
     if (RPW > 64) return set_error(SLLM_ERR_SHAPE, "gemv: more than 64 rows per wave (rows too many)");
-    const int64_t waves = ((int64_t)N + RPW - 1) / RPW;
+    const int64_t waves = count_waves(RPW);
+    int W = (int)((waves + wgs - 1) / wgs);
+    W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
     const int grid = (int)((waves + W - 1) / W);
+    SegTable S{};
+    S.n = nseg;
+    S.wave0[0] = 0;
+    for (int i = 0; i < nseg; i++) {
+        S.P[i] = P[i];
+        S.N[i] = N[i];
+        S.wave0[i + 1] = S.wave0[i] + (N[i] + RPW - 1) / RPW;
+    }
+    S.wave0[nseg] = grid * W;  // the last segment also takes the spare waves
     const int U = RPW * KCH;
     int done = 0;
     while (done < M) {
@@ -471,24 +519,29 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
         const int64_t unit_bytes = (int64_t)64 * NB * plane_block_bytes(fmt);
         const int64_t inflight = (int64_t)T.gemv_inflight_kb * 1024;
         int D = 1;
-        while (D * 2 * NB * MT <= 8 && D < U && (int64_t)waves * unit_bytes * D * 2 <= inflight) D *= 2;
+        while (D * 2 * NB * MT <= 8 && D < U && waves * unit_bytes * D * 2 <= inflight) D *= 2;
         const int mrows = left < MT ? left : MT;
         const size_t lds = act_lds_bytes(fmt, MT, G);
         const float *xp = x + (size_t)done * G * 32;
-        float *dp = dst + (size_t)done * N;
+        for (int i = 0; i < nseg; i++) S.dst[i] = dst[i] + (size_t)done * N[i];
         sllm_status st;
         switch (fmt) {
-        case SLLM_Q8_0: st = launch_mt<SLLM_Q8_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q4_0: st = launch_mt<SLLM_Q4_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q4_1: st = launch_mt<SLLM_Q4_1>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q5_0: st = launch_mt<SLLM_Q5_0>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q5K1: st = launch_mt<SLLM_Q5K1>(MT, NB, D, P, xp, dp, N, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q8_0: st = launch_mt<SLLM_Q8_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q4_0: st = launch_mt<SLLM_Q4_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q4_1: st = launch_mt<SLLM_Q4_1>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q5_0: st = launch_mt<SLLM_Q5_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q5K1: st = launch_mt<SLLM_Q5K1>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");
         }
         if (st != SLLM_OK) return st;
         done += mrows;
     }
     return SLLM_OK;
+}
+
+sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                        hipStream_t s) {
+    return launch_gemv_multi(fmt, &P, &dst, &N, 1, x, G, M, s);
 }
 
 // ------------------------------------------------------ verification ----

@@ -89,6 +89,11 @@ sllm_status hip_error(hipError_t e, const char *what);
 // Kernel launch helpers implemented in the .hip files.
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         hipStream_t s);
+// One GEMV launch over up to kMaxSegs weights of one format and one K that
+// share the activation rows x: weight i (N[i] rows) writes dst[i] (M x N[i]).
+constexpr int kMaxSegs = 4;
+sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
+                              const float *x, int G, int M, hipStream_t s);
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         void *ws, size_t ws_bytes, hipStream_t s);
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M);

@@ -79,6 +79,8 @@ def lib() -> C.CDLL:
     L.sllm_matmul_quant_into_f32.argtypes = [W, P, i32, i32, P]
     L.sllm_matmul_row_quant_into_f32.argtypes = [W, P, P]
     L.sllm_matmul_dev.argtypes = [W, P, i32, i32, P, P]
+    L.sllm_matmul_multi_quant_into_f32.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P)]
+    L.sllm_matmul_multi_dev.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P), P]
     L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
     L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
@@ -237,6 +239,27 @@ def matmul_dev(w: DeviceWeight, x_ptr: int, x_rows: int, x_cols: int, dst_ptr: i
     """Device-resident matmul: raw device pointers, enqueued on `stream`."""
     _check(lib().sllm_matmul_dev(w.handle, C.c_void_p(x_ptr), x_rows, x_cols, C.c_void_p(dst_ptr),
                                  C.c_void_p(stream)))
+
+
+def model_matmul_multi_quant_into_f32(ws: list, x_data: np.ndarray, x_rows: int, x_cols: int) -> list:
+    """Consecutive modelMatmulIntoF32 calls on one input (forwardBlock's q/k/v,
+    model_f32.go:391-396, and gate/up, :479-482) in one call: returns one
+    (x_rows * Rows) array per weight, as the single calls would."""
+    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    if x.size < x_rows * x_cols:
+        raise SllmError(1, "xData shorter than xRows*xCols")
+    outs = [np.empty(x_rows * w.rows, np.float32) for w in ws]
+    hs = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+    ds = (C.c_void_p * len(ws))(*[_ptr(o) for o in outs])
+    _check(lib().sllm_matmul_multi_quant_into_f32(hs, len(ws), _ptr(x), x_rows, x_cols, ds))
+    return outs
+
+
+def matmul_multi_dev(ws: list, x_ptr: int, x_rows: int, x_cols: int, dst_ptrs: list, stream: int = 0) -> None:
+    """Device-resident multi-weight matmul on one activation input."""
+    hs = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+    ds = (C.c_void_p * len(ws))(*[C.c_void_p(p) for p in dst_ptrs])
+    _check(lib().sllm_matmul_multi_dev(hs, len(ws), C.c_void_p(x_ptr), x_rows, x_cols, ds, C.c_void_p(stream)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

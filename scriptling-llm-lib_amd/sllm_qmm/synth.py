@@ -16,30 +16,45 @@ _M1 = np.uint64(0xBF58476D1CE4E5B9)
 _M2 = np.uint64(0x94D049BB133111EB)
 
 
-def splitmix64(seed: int, n: int) -> np.ndarray:
-    """n consecutive SplitMix64 outputs for `seed`."""
+def splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start .. start + n - 1 of the SplitMix64 stream for `seed`."""
     with np.errstate(over="ignore"):
-        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + np.arange(1, n + 1, dtype=np.uint64) * _GOLDEN
-        z = (z ^ (z >> np.uint64(30))) * _M1
-        z = (z ^ (z >> np.uint64(27))) * _M2
-        return z ^ (z >> np.uint64(31))
+        z = np.arange(start + 1, start + n + 1, dtype=np.uint64)
+        z *= _GOLDEN
+        z += np.uint64(seed & 0xFFFFFFFFFFFFFFFF)
+        z ^= z >> np.uint64(30)
+        z *= _M1
+        z ^= z >> np.uint64(27)
+        z *= _M2
+        z ^= z >> np.uint64(31)
+        return z
 
 
-def uniform(seed: int, n: int) -> np.ndarray:
+def uniform(seed: int, n: int, start: int = 0) -> np.ndarray:
     """n doubles in [0, 1) from the top 53 bits."""
-    return (splitmix64(seed, n) >> np.uint64(11)).astype(np.float64) * (1.0 / (1 << 53))
+    u = splitmix64(seed, n, start)
+    u >>= np.uint64(11)
+    f = u.astype(np.float64)
+    f *= 1.0 / (1 << 53)
+    return f
 
 
-def normal(seed: int, n: int, std: float = 1.0) -> np.ndarray:
-    """n float32 ~ N(0, std^2) by Box-Muller over consecutive uniform pairs."""
+def normal(seed: int, n: int, std: float = 1.0, chunk: int = 1 << 20) -> np.ndarray:
+    """n float32 ~ N(0, std^2) by Box-Muller over consecutive uniform pairs
+    (generated in chunks of `chunk` pairs; the values do not depend on it)."""
     m = (n + 1) // 2
-    u = uniform(seed, 2 * m)
-    r = np.sqrt(-2.0 * np.log1p(-u[0::2]))
-    t = 2.0 * np.pi * u[1::2]
-    z = np.empty(2 * m, np.float64)
-    z[0::2] = r * np.cos(t)
-    z[1::2] = r * np.sin(t)
-    return (z[:n] * std).astype(np.float32)
+    out = np.empty(2 * m, np.float32)
+    for p0 in range(0, m, chunk):
+        p1 = min(m, p0 + chunk)
+        u = uniform(seed, 2 * (p1 - p0), 2 * p0)
+        r = np.sqrt(-2.0 * np.log1p(-u[0::2]))
+        t = 2.0 * np.pi * u[1::2]
+        z = np.empty(2 * (p1 - p0), np.float64)
+        z[0::2] = r * np.cos(t)
+        z[1::2] = r * np.sin(t)
+        z *= std
+        out[2 * p0:2 * p1] = z
+    return out[:n]
 
 
 def random_bytes(seed: int, n: int) -> np.ndarray:

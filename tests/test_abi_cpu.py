@@ -46,6 +46,11 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_weight_from_gguf(12, p, 16, 1, 256, C.byref(h)) == 1                    # too short
     assert lib.sllm_matmul_quant_into_f32(None, p, 1, 32, p) == 1
     assert lib.sllm_set_param(b"no_such_knob", 3) == 1
+    assert lib.sllm_matmul_multi_quant_into_f32(None, 1, p, 1, 32, None) == 1
+    hs = (C.c_void_p * 1)(None)
+    ds = (C.c_void_p * 1)(p)
+    assert lib.sllm_matmul_multi_quant_into_f32(hs, 0, p, 1, 32, ds) == 1                 # count 0
+    assert lib.sllm_matmul_multi_dev(hs, 1, p, 1, 32, ds, None) == 1                        # null weight
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
@@ -64,5 +69,6 @@ def test_no_gpu_is_a_device_error_not_a_fallback():
 def test_python_host_mirror_names():
     # the Go entry points this path replaces, mirrored by the host module
     for name in ("QuantWeight", "load_weight_f32_direct", "quantize_q8_rows_f32",
-                 "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev"):
+                 "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev",
+                 "model_matmul_multi_quant_into_f32"):
         assert hasattr(sq, name)
