@@ -84,6 +84,25 @@ __device__ __forceinline__ int group_sum(int v) {
 // over |x| (NaN never wins the `>` compare), scale = maxAbs/127 and inv =
 // 1/scale in IEEE fp32 (0 for an all-zero block), q = clamp(int32(x*inv)).
 // The maximum and the integer sum do not depend on how the lanes combine.
+//
+// Per element this is quant_trunc_clamp(x * inv) in fewer operations: the
+// product is clamped in float first (fmaxf returns -128 for a NaN product,
+// and trunc(clamp(t)) == clamp(trunc(t)) for every finite or infinite t), then
+// truncated. The one case where the two differ is a +Inf product, which Go
+// sends to INT32_MIN and so to -128: x * inv is +Inf only when inv itself is
+// +Inf (the block's scale underflowed to 0 or below 1/FLT_MAX), and then every
+// product of the block is +-Inf or NaN, so the whole block codes to -128.
+__device__ __forceinline__ int quant_clamped(float p) {
+    const float t = __builtin_fminf(__builtin_fmaxf(p, -128.0f), 127.0f);
+    return (int)t;
+}
+// Low bytes of four ints packed into one word (element 0 in byte 0).
+__device__ __forceinline__ int pack4(int q0, int q1, int q2, int q3) {
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)q1, (uint32_t)q0, 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)q3, (uint32_t)q2, 0x0c0c0400u);
+    return (int)__builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
 template <int TPB>
 __device__ __forceinline__ void quantize_part(const float4 *v, int *w, float &scale, int &sum) {
     float a = 0.0f;
@@ -101,14 +120,13 @@ __device__ __forceinline__ void quantize_part(const float4 *v, int *w, float &sc
         s = a / 127.0f;
         inv = 1.0f / s;
     }
+    const bool inf_inv = inv == __builtin_inff();
     int sm = 0;
 #pragma unroll
     for (int k = 0; k < 8 / TPB; k++) {
-        const int q0 = quant_trunc_clamp(v[k].x * inv);
-        const int q1 = quant_trunc_clamp(v[k].y * inv);
-        const int q2 = quant_trunc_clamp(v[k].z * inv);
-        const int q3 = quant_trunc_clamp(v[k].w * inv);
-        w[k] = (q0 & 0xff) | ((q1 & 0xff) << 8) | ((q2 & 0xff) << 16) | (int)((uint32_t)(q3 & 0xff) << 24);
+        w[k] = pack4(quant_clamped(v[k].x * inv), quant_clamped(v[k].y * inv), quant_clamped(v[k].z * inv),
+                     quant_clamped(v[k].w * inv));
+        w[k] = inf_inv ? (int)0x80808080u : w[k];
         sm = __builtin_amdgcn_sdot4(w[k], 0x01010101, sm, false);
     }
     scale = s;

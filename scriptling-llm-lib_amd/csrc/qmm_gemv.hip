@@ -1,442 +1,29 @@
-// Decode GEMV (xRows < 64) for every weight format.
-//
-// Persistent launch (at most gemv_wg_per_cu workgroups per CU). Each wave owns
-// rows wv, wv + TW, ... and streams them as units of NB blocks per lane (one
-// K-chunk of a row), keeping D units in flight in a register ring.
-//   1. threads that own an activation block issue its loads first, then every
-//      wave issues its first D units of weight loads, then the owners quantize
-//      their block into LDS with the bit-exact Q8_0 quantizer (Q5_0: stage the
-//      fp32 block) - the weight stream is in flight during the prologue;
-//   2. main loop: lane l owns blocks l + 64 i of each K-chunk; it reads the
-//      block's activation codes from LDS, forms the reference's per-block term
-//      exactly and accumulates; at a row's end the wave reduces across lanes
-//      (fixed order) and parks the sum in lane (row ordinal); results are
-//      stored once at the end, one coalesced store per wave.
-// The per-block term equals the reference's bit for bit; only the order in
-// which a row's terms are added differs from the reference's sequential loop
-// (reassociation), and that order is fixed, so results are reproducible.
+// Decode GEMV (xRows < 64) planner: launch shapes for one or several weights
+// sharing their activation rows, and the verification kernels. The kernel
+// templates are in qmm_gemv_kernel.hpp; each weight format's launch chain is
+// instantiated in its own translation unit (qmm_gemv_<fmt>.hip).
 #include <hip/hip_runtime.h>
 
-#include "qmm_device.hpp"
-#include "qmm_internal.hpp"
+#include "qmm_gemv_kernel.hpp"
 
 namespace sllm {
 
+namespace gemv {
+extern template sllm_status launch_mt<SLLM_Q8_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
+                                                 int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
+                                                 int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_1>(int, int, int, const SegTable &, const float *, int, int, int, int,
+                                                 int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
+                                                 int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5K1>(int, int, int, const SegTable &, const float *, int, int, int, int,
+                                                 int, int, size_t, hipStream_t);
+}  // namespace gemv
+
+using namespace gemv;
+
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-// Weight planes are read once per GEMV: non-temporal loads keep them from
-// displacing the activations and other reused data in L2 / MALL.
-__device__ __forceinline__ int4 ld_nt(const int4 *p) {
-    const v4i t = __builtin_nontemporal_load((const v4i *)p);
-    return make_int4(t.x, t.y, t.z, t.w);
-}
-__device__ __forceinline__ uint16_t ld_nt(const uint16_t *p) { return __builtin_nontemporal_load(p); }
-__device__ __forceinline__ uint32_t ld_nt(const uint32_t *p) { return __builtin_nontemporal_load(p); }
-
-// LDS image of the prologue for MT activation rows of G blocks.
-struct ActView {
-    int4 *xl;   // [MT][G] elements 0..15 of each block (int8)
-    int4 *xh;   // [MT][G] elements 16..31
-    float *xs;  // [MT][G] activation scale
-    int *sx;    // [MT][G] Σxq
-    float *xf;  // Q5_0: [MT][G][kXfStride] fp32 activations
-};
-
-__host__ __device__ inline size_t act_lds_bytes(int fmt, int MT, int G) {
-    if (fmt == SLLM_Q5_0) return (size_t)MT * G * kXfStride * sizeof(float);
-    return (size_t)MT * G * (2 * sizeof(int4) + sizeof(float) + sizeof(int));
-}
-
-__device__ inline ActView carve_act(unsigned char *lds, int fmt, int MT, int G) {
-    ActView v{};
-    if (fmt == SLLM_Q5_0) {
-        v.xf = (float *)lds;
-    } else {
-        v.xl = (int4 *)lds;
-        v.xh = v.xl + (size_t)MT * G;
-        v.xs = (float *)(v.xh + (size_t)MT * G);
-        v.sx = (int *)(v.xs + (size_t)MT * G);
-    }
-    return v;
-}
-
-// Writes one lane's part (8/TPB float4 = 32/TPB elements) of activation block
-// blk into LDS: quantized codes + scale + Σq, or (Q5_0) the fp32 values.
-template <int FMT, int TPB>
-__device__ __forceinline__ void stage_part(const float4 *v, int blk, int sub, const ActView &A) {
-    constexpr int NV = 8 / TPB;
-    if (FMT == SLLM_Q5_0) {
-        float4 *d = (float4 *)(A.xf + (size_t)blk * kXfStride) + sub * NV;
-#pragma unroll
-        for (int k = 0; k < NV; k++) d[k] = v[k];
-    } else {
-        int w[NV];
-        float s;
-        int sm;
-        quantize_part<TPB>(v, w, s, sm);
-        // word j of the block (j = sub*NV + k): words 0..3 -> xl, 4..7 -> xh
-        int *lo = (int *)(A.xl + blk), *hi = (int *)(A.xh + blk);
-#pragma unroll
-        for (int k = 0; k < NV; k++) {
-            const int j = sub * NV + k;
-            if (j < 4) lo[j] = w[k];
-            else hi[j - 4] = w[k];
-        }
-        if (sub == 0) {
-            A.xs[blk] = s;
-            A.sx[blk] = sm;
-        }
-    }
-}
-
-// Per-lane register image of one weight block.
-struct BlockRegs {
-    int4 q, q2;
-    uint16_t d, m, dh;
-    uint32_t qh;
-};
-
-template <class T>
-__device__ __forceinline__ const T *at(const T *base, uint32_t idx) {
-    // base + 32-bit byte offset: lets the loads use the SGPR-base + VGPR-offset form
-    return (const T *)((const char *)base + (uint64_t)(idx * (uint32_t)sizeof(T)));
-}
-
-template <int FMT>
-__device__ __forceinline__ void load_block(const Planes &P, uint32_t idx, BlockRegs &b) {
-    b.q = ld_nt(at(P.qs, idx));
-    b.d = ld_nt(at(P.d, idx));
-    if (FMT == SLLM_Q8_0) b.q2 = ld_nt(at(P.qs2, idx));
-    if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) b.m = ld_nt(at(P.m, idx));
-    if (FMT == SLLM_Q5K1) b.dh = ld_nt(at(P.dh, idx));
-    if (FMT == SLLM_Q5_0 || FMT == SLLM_Q5K1) b.qh = ld_nt(at(P.qh, idx));
-}
-
-// Blocks lane + 64 i (i < NB) of one unit, starting at plane index `base`.
-template <int FMT, int NB>
-__device__ __forceinline__ void load_unit(const Planes &P, BlockRegs (&u)[NB], uint32_t base) {
-#pragma unroll
-    for (int i = 0; i < NB; i++) load_block<FMT>(P, base + 64u * i, u[i]);
-}
-
-// Activation operands of one block, read from LDS.
-struct ActRegs {
-    int4 xl, xh;
-    float xs;
-    int sx;
-    float4 xf[8];
-};
-
-template <int FMT>
-__device__ __forceinline__ void load_act(const ActView &A, size_t a, ActRegs &r) {
-    if (FMT == SLLM_Q5_0) {
-        const float4 *src = (const float4 *)(A.xf + a * kXfStride);
-#pragma unroll
-        for (int k = 0; k < 8; k++) r.xf[k] = src[k];
-    } else {
-        r.xl = A.xl[a];
-        r.xh = A.xh[a];
-        r.xs = A.xs[a];
-        r.sx = A.sx[a];
-    }
-}
-
-// Adds one block's term to acc (acc2: the Q5K1 high half), in the reference's
-// operation order for that format.
-template <int FMT>
-__device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x, float &acc, float &acc2) {
-    if (FMT == SLLM_Q5_0) {
-        const float sum = q5_block_sum(b.q, b.qh, x.xf);
-        const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`
-        acc = acc + grp;
-    } else if (FMT == SLLM_Q8_0) {
-        // q8q8.go:187-195 + vnni_amd64.s:70-73: cmb = ws*xs, term = float(isum)*cmb
-        const int isum = q8_isum(b.q, b.q2, x.xl, x.xh);
-        const float cmb = f16_lut(b.d) * x.xs;
-        const float term = cmb * (float)isum;
-        acc = acc + term;
-    } else if (FMT == SLLM_Q4_0) {
-        // q4q8.go:37-43: ws*xs*float(Σ(nib-8)·xq); Σ(nib-8)xq = Σnib·xq - 8Σxq exactly
-        const int isum = nib_isum(b.q, x.xl, x.xh) - 8 * x.sx;
-        const float cmb = f16_exact(b.d) * x.xs;
-        const float term = cmb * (float)isum;
-        acc = acc + term;
-    } else {
-        // q41q8_row_amd64.s:65-71: ((float(qsum)*d) + (float(Σxq)*m)) * xs
-        const float fsx = (float)x.sx;
-        const int qsum = nib_isum(b.q, x.xl, x.xh);
-        const float t1 = (float)qsum * f16_exact(b.d);
-        const float t2 = fsx * f16_exact(b.m);
-        float t = t1 + t2;
-        t = t * x.xs;
-        acc = acc + t;
-        if (FMT == SLLM_Q5K1) {
-            // high Q4_1 block of convertQ5KToTwoQ41: scale dh, min +0, 0/1 codes
-            const int hsum = bits_isum(b.qh, x.xl, x.xh);
-            const float h1 = (float)hsum * f16_exact(b.dh);
-            const float h2 = fsx * 0.0f;
-            float h = h1 + h2;
-            h = h * x.xs;
-            acc2 = acc2 + h;
-        }
-    }
-}
-
-// Sum over the 64 lanes of a wave with DPP moves (no LDS round trips), in a
-// fixed order: pairs, quads, 8-lane and 16-lane rows within each row of 16
-// lanes, then the four row sums (lanes 0, 16, 32, 48) added left to right.
-// Every lane receives the result.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-    const int m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
-    return v + __builtin_bit_cast(float, m);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
-    v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]: lane ^ 2
-    v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of each 8 lanes
-    v = dpp_add<0x140>(v);  // row_mirror: the other 8 lanes of each row of 16
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return ((r0 + r1) + r2) + r3;
-}
-
-template <int FMT, int NB, int D, int TPB, class NextBase>
-__device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB], const float *__restrict__ x,
-                                         int M, int G, const ActView &A, NextBase &next_base) {
-    constexpr int NV = 8 / TPB;  // float4 per thread per block
-    const int nblk = M * G;
-    const int per_pass = blockDim.x / TPB;
-    const int blk = threadIdx.x / TPB, sub = threadIdx.x % TPB;
-    if (blk < nblk) {
-        float4 xv[NV];
-        const float4 *src = (const float4 *)(x + (size_t)blk * 32) + sub * NV;
-#pragma unroll
-        for (int k = 0; k < NV; k++) xv[k] = src[k];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
-        __builtin_amdgcn_sched_barrier(0);
-        stage_part<FMT, TPB>(xv, blk, sub, A);
-    } else {
-#pragma unroll
-        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
-    }
-    for (int b = blk + per_pass; b < nblk; b += per_pass) {
-        float4 v[NV];
-        const float4 *src = (const float4 *)(x + (size_t)b * 32) + sub * NV;
-#pragma unroll
-        for (int k = 0; k < NV; k++) v[k] = src[k];
-        stage_part<FMT, TPB>(v, b, sub, A);
-    }
-}
-
-// The weights of one launch (same format, same K, same activation rows).
-// Segment s owns the waves [wave0[s], wave0[s + 1]) of the grid; wave0[n] is
-// the grid's wave count, so the last segment also takes the spare waves.
-struct SegTable {
-    Planes P[kMaxSegs];
-    float *dst[kMaxSegs];
-    int N[kMaxSegs];
-    int wave0[kMaxSegs + 1];
-    int n;
-};
-
-// A wave's work is a stream of units: unit t is K-chunk (t % KCH) of its row
-// number (t / KCH), rows being wv, wv + TW, ... of its segment's weight (at
-// most RPW of them). A unit is NB blocks per lane. The wave keeps D units in
-// flight in a register ring: it computes unit t, then issues the loads of
-// unit t + D into the registers it just consumed.
-template <int FMT, int NB, int D, int MT, bool HOIST>
-__global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__restrict__ x, int G, int M,
-                                                    int KCH, int RPW, int tpb) {
-    extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
-    const ActView A = carve_act(lds, FMT, MT, G);
-    const int lane = threadIdx.x & 63;
-    const int W = blockDim.x >> 6;
-    // this wave's segment (wave-uniform, so the selection stays in scalar registers)
-    const int wg = __builtin_amdgcn_readfirstlane(blockIdx.x * W + (threadIdx.x >> 6));
-    Planes P = S.P[0];
-    float *__restrict__ dst = S.dst[0];
-    int N = S.N[0], w0 = 0, w1 = S.wave0[1];
-#pragma unroll
-    for (int s = 1; s < kMaxSegs; s++) {
-        if (s < S.n && wg >= S.wave0[s]) {
-            P = S.P[s];
-            dst = S.dst[s];
-            N = S.N[s];
-            w0 = S.wave0[s];
-            w1 = S.wave0[s + 1];
-        }
-    }
-    const int TW = w1 - w0;
-    const int wv = wg - w0;
-    const int U = RPW * KCH;
-    constexpr int CH = 64 * NB;  // blocks per K-chunk
-
-    // Load-stream position (row ordinal lq, chunk lk). Units past this wave's
-    // last real unit (ring padding) re-read that last unit: the data is still
-    // in flight or in cache, and no two waves pile onto the same lines.
-    const int real_rows = wv < N ? (N - 1 - wv) / TW + 1 : 0;
-    const int U_real = real_rows * KCH;
-    int lq = 0, lk = 0, lt = 0;
-    uint32_t last = (uint32_t)min(wv, N - 1) * (uint32_t)G + (uint32_t)lane;
-    auto next_base = [&]() -> uint32_t {
-        if (lt >= U_real) return last;
-        const int row = wv + lq * TW;
-        last = (uint32_t)row * (uint32_t)G + (uint32_t)(lk * CH + lane);
-        ++lt;
-        if (++lk == KCH) {
-            lk = 0;
-            ++lq;
-        }
-        return last;
-    };
-
-    BlockRegs buf[D][NB];
-    // Prologue: the activation rows (M x G blocks) are quantized by all
-    // threads, TPB lanes per block. Each thread issues its activation loads,
-    // then its wave's first D units of weights, then quantizes: it waits only
-    // for its activation loads while the weight stream is in flight.
-    switch (tpb) {
-    case 8: prologue<FMT, NB, D, 8>(P, buf, x, M, G, A, next_base); break;
-    case 4: prologue<FMT, NB, D, 4>(P, buf, x, M, G, A, next_base); break;
-    case 2: prologue<FMT, NB, D, 2>(P, buf, x, M, G, A, next_base); break;
-    default: prologue<FMT, NB, D, 1>(P, buf, x, M, G, A, next_base); break;
-    }
-    __syncthreads();
-
-    float acc[MT], acc2[MT], res[MT];
-#pragma unroll
-    for (int m = 0; m < MT; m++) acc[m] = acc2[m] = res[m] = 0.0f;
-    int cq = 0, ck = 0;  // compute-stream position
-
-    // HOIST (a row is one K-chunk): every unit uses the same blocks, so the
-    // activation operands are read from LDS once, before the loop.
-    ActRegs xh[HOIST ? NB : 1][HOIST ? MT : 1];
-    if (HOIST) {
-#pragma unroll
-        for (int i = 0; i < NB; i++)
-#pragma unroll
-            for (int m = 0; m < MT; m++)
-                if (m < M) load_act<FMT>(A, (size_t)m * G + min(lane + 64 * i, G - 1), xh[HOIST ? i : 0][HOIST ? m : 0]);
-    }
-
-    // consume one unit from ring slot d
-    auto compute = [&](BlockRegs (&u)[NB]) {
-#pragma unroll
-        for (int i = 0; i < NB; i++) {
-            const int g = ck * CH + lane + 64 * i;
-            if (g < G) {
-#pragma unroll
-                for (int m = 0; m < MT; m++) {
-                    if (m >= M) continue;
-                    if (HOIST) {
-                        block_term<FMT>(u[i], xh[HOIST ? i : 0][HOIST ? m : 0], acc[m], acc2[m]);
-                    } else {
-                        ActRegs xa;
-                        load_act<FMT>(A, (size_t)m * G + g, xa);
-                        block_term<FMT>(u[i], xa, acc[m], acc2[m]);
-                    }
-                }
-            }
-        }
-        if (++ck == KCH) {
-            // row done: reduce across the wave (fixed order), park it in lane cq
-#pragma unroll
-            for (int m = 0; m < MT; m++) {
-                float v = wave_sum(acc[m]);
-                if (FMT == SLLM_Q5K1) v = v + wave_sum(acc2[m]);
-                res[m] = (lane == cq) ? v : res[m];
-                acc[m] = acc2[m] = 0.0f;
-            }
-            ck = 0;
-            ++cq;
-        }
-    };
-
-    // Ueff: units rounded up to whole rings (the tail units are clamped
-    // repeats of the last row; their results land in lanes >= RPW and are
-    // dropped). Loads are unconditional in the steady state so the compiler
-    // waits exactly for the unit being consumed.
-    const int Ueff = (U + D - 1) / D * D;
-    for (int t0 = 0; t0 + D < Ueff; t0 += D) {
-#pragma unroll
-        for (int d = 0; d < D; d++) {
-            compute(buf[d]);
-            load_unit<FMT, NB>(P, buf[d], next_base());
-        }
-    }
-#pragma unroll
-    for (int d = 0; d < D; d++) compute(buf[d]);
-
-    const int row = wv + lane * TW;
-    if (lane < RPW && row < N) {
-#pragma unroll
-        for (int m = 0; m < MT; m++)
-            if (m < M) dst[(size_t)m * N + row] = res[m];
-    }
-}
-
-template <int FMT, int NB, int D, int MT>
-sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
-                     size_t lds, hipStream_t s) {
-    // hoisting needs room for the operands: not for Q5_0 (32 fp32 per block)
-    constexpr bool kCanHoist = FMT != SLLM_Q5_0 && NB * MT <= 4;
-    // lanes per activation block in the prologue: as many as the workgroup allows
-    int tpb = 8;
-    while (tpb > 1 && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
-    if (kCanHoist && KCH == 1)
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M,
-                           KCH, RPW, tpb);
-    else
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M, KCH,
-                           RPW, tpb);
-    SLLM_HIP(hipGetLastError());
-    return SLLM_OK;
-}
-
-// D units in flight; NB * D * MT <= 8 blocks per lane.
-template <int FMT, int NB, int MT>
-sllm_status launch_d(int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
-                     size_t lds, hipStream_t s) {
-    constexpr int DMAX = 8 / (NB * MT) >= 8 ? 8 : (8 / (NB * MT) >= 4 ? 4 : (8 / (NB * MT) >= 2 ? 2 : 1));
-    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    return launch_t<FMT, NB, 1, MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-}
-
-template <int FMT, int MT>
-sllm_status launch_nb(int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W,
-                      int grid, size_t lds, hipStream_t s) {
-    switch (NB) {
-    case 1: return launch_d<FMT, 1, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_d<FMT, 2, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 3: return launch_d<FMT, 3, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_d<FMT, 4, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 5: return launch_d<FMT, 5, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 6: return launch_d<FMT, 6, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 7: return launch_d<FMT, 7, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 8: return launch_d<FMT, 8, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    }
-    return set_error(SLLM_ERR_SHAPE, "gemv: unsupported blocks-per-lane");
-}
-
-template <int FMT>
-sllm_status launch_mt(int MT, int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW,
-                      int W, int grid, size_t lds, hipStream_t s) {
-    switch (MT) {
-    case 1: return launch_nb<FMT, 1>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_nb<FMT, 2>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_nb<FMT, 4>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    }
-    return set_error(SLLM_ERR_SHAPE, "gemv: unsupported row tile");
-}
 
 constexpr size_t kMaxLds = 64 * 1024;
 
@@ -466,18 +53,6 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
     }
     const Tuning &T = tuning();
     const int64_t wgs = (int64_t)device_cus() * T.gemv_wg_per_cu;
-    // Blocks per lane per unit. Rows of up to 8 x 64 blocks are one unit
-    // (one K-chunk, issued at once); longer rows are split into K-chunks of
-    // the largest lane-group count <= 8 that divides them (no partial chunks).
-    const int lg = (G + 63) / 64;
-    const int nb_cap = T.gemv_max_nb;
-    int NB = lg;
-    if (lg > nb_cap) {
-        NB = nb_cap;
-        while (NB > 1 && lg % NB) NB--;
-        if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
-    }
-    const int KCH = (G + 64 * NB - 1) / (64 * NB);
     // Rows per wave: the fewest that fit every segment's rows into
     // gemv_waves waves per workgroup slot. Each segment gets just enough waves
     // for that many rows each; the waves per workgroup are then the fewest
@@ -492,6 +67,26 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
     while (count_waves(RPW) > slots) RPW++;
     if (RPW > 64) return set_error(SLLM_ERR_SHAPE, "gemv: more than 64 rows per wave (rows too many)");
     const int64_t waves = count_waves(RPW);
+    // Blocks per lane per unit (NB) and K-chunks per row (KCH). Rows of up to
+    // gemv_max_nb x 64 blocks are one chunk; longer rows are split into chunks
+    // of the largest lane-group count that divides them (no partial chunks).
+    // While a wave would stream fewer than 4 units, its rows are split further,
+    // so that it overlaps its loads with its compute instead of issuing
+    // everything at once and doing all its compute after the last byte lands.
+    const int lg = (G + 63) / 64;
+    const int nb_cap = T.gemv_max_nb;
+    int NB = lg;
+    if (lg > nb_cap) {
+        NB = nb_cap;
+        while (NB > 1 && lg % NB) NB--;
+        if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
+    }
+    while (NB > 1 && RPW * ((lg + NB - 1) / NB) < 4) {
+        int nb = NB - 1;
+        while (nb > 1 && lg % nb) nb--;
+        NB = nb;
+    }
+    const int KCH = (G + 64 * NB - 1) / (64 * NB);
     int W = (int)((waves + wgs - 1) / wgs);
     W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
     const int grid = (int)((waves + W - 1) / W);
@@ -513,13 +108,13 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
         if (act_lds_bytes(fmt, MT, G) > kMaxLds)
             return set_error(SLLM_ERR_SHAPE, "gemv: activation row does not fit in LDS");
         // ring depth: units in flight per wave, bounded by registers (NB*D*MT
-        // <= 8 blocks per lane), by the wave's unit count, and by the bytes in
+        // <= 8 blocks per lane), by the wave's unit count (D <= U), and by the bytes in
         // flight over the whole device (enough to cover HBM latency; more only
         // piles compute into the tail)
         const int64_t unit_bytes = (int64_t)64 * NB * plane_block_bytes(fmt);
         const int64_t inflight = (int64_t)T.gemv_inflight_kb * 1024;
         int D = 1;
-        while (D * 2 * NB * MT <= 8 && D < U && waves * unit_bytes * D * 2 <= inflight) D *= 2;
+        while (D * 2 * NB * MT <= 8 && D * 2 <= U && waves * unit_bytes * D * 2 <= inflight) D *= 2;
         const int mrows = left < MT ? left : MT;
         const size_t lds = act_lds_bytes(fmt, MT, G);
         const float *xp = x + (size_t)done * G * 32;
