@@ -1,4 +1,5 @@
-// Prefill GEMM (xRows >= 64) on the int8 matrix cores.
+// Prefill GEMM (xRows >= 64): int8 matrix cores for Q8_0 / Q4_0 / Q4_1 / Q5K1,
+// and a VALU GEMM for Q5_0 (fp32 activations; see gemm_q5_kernel below).
 //
 // 1. The activation rows are quantized once into a workspace (xq int8 [M][K],
 //    xs fp32 [M][G], Σxq int32 [M][G]) by the GEMV prologue's routine.
@@ -338,6 +339,167 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
     }
 }
 
+// ------------------------------------------------------------- Q5_0 ----
+//
+// Q5_0 keeps fp32 activations (no int8 operand, float32_ops.go:427-436), so
+// its prefill GEMM runs on the VALU. Each output's per-block sum is formed in
+// the reference's operation order (q5DotGroupXF32, float32_ops.go:335-367):
+// for j = 0..15, p0 = v0*x[j], p1 = v1*x[j+16], sum = sum + (p0 + p1), with
+// v = float(q5) - 16; then term = d * sum, accumulated block by block. That
+// is two fp32 VALU ops per weight and activation, so the VALU bounds it.
+// A workgroup of 256 threads owns a 64 x 64 tile of dst; thread (tm, tn)
+// owns activation rows tm + 16 r and weight rows tn + 16 c (r, c < 4). Per
+// block the x tile and the decoded weight tile (fp32) are staged in LDS,
+// double-buffered: the next block's global loads are in flight during the
+// current block's arithmetic.
+constexpr int kQ5Tile = 64;
+constexpr int kQ5Stride = 36;  // floats per LDS row: 16-byte aligned, rows spread over the banks
+
+struct alignas(16) Q5Stage {
+    float x[kQ5Tile * kQ5Stride];
+    float v[kQ5Tile * kQ5Stride];
+    float d[kQ5Tile];
+};
+
+// This thread's share of one block's global operands: two float4 of x (rows
+// t/8 and t/8 + 32) and four nibble bytes + high bits + scale of weight row t/4.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+struct Q5Fetch {
+    v4f x0, x1;
+    uint32_t qs, qh;
+    uint16_t d;
+};
+
+__device__ __forceinline__ void q5_fetch(const Planes &P, const float *__restrict__ x, int M, int N, int G, int m0,
+                                         int n0, int g, Q5Fetch &f) {
+    const int t = threadIdx.x;
+    // rows past M / N load the last row again; their outputs are not stored
+    const int r = t >> 3, c = t & 7;
+    const int ma = min(m0 + r, M - 1), mb = min(m0 + r + 32, M - 1);
+    f.x0 = *((const v4f *)(x + ((size_t)ma * G + g) * 32) + c);
+    f.x1 = *((const v4f *)(x + ((size_t)mb * G + g) * 32) + c);
+    const int n = min(n0 + (t >> 2), N - 1);
+    const size_t idx = (size_t)n * G + g;
+    f.qs = ((const uint32_t *)(P.qs + idx))[t & 3];
+    f.qh = P.qh[idx];
+    f.d = P.d[idx];
+}
+
+__device__ __forceinline__ void q5_store(Q5Stage &S, const Q5Fetch &f) {
+    const int t = threadIdx.x;
+    const int r = t >> 3, c = t & 7;
+    *(v4f *)(S.x + r * kQ5Stride + 4 * c) = f.x0;
+    *(v4f *)(S.x + (r + 32) * kQ5Stride + 4 * c) = f.x1;
+    // weight row t/4, elements 4 part .. 4 part + 3 (low nibbles) and 16 + those
+    // (high nibbles); bit e of qh is bit 4 of element e (gguf.go:472-490)
+    const int row = t >> 2, part = t & 3;
+    float lo[4], hi[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int e = 4 * part + i;
+        const uint32_t b = (f.qs >> (8 * i)) & 0xffu;
+        const int q0 = (int)((b & 0x0fu) | (((f.qh >> e) & 1u) << 4));
+        const int q1 = (int)((b >> 4) | (((f.qh >> (e + 16)) & 1u) << 4));
+        lo[i] = (float)q0 - 16.0f;
+        hi[i] = (float)q1 - 16.0f;
+    }
+    *(v4f *)(S.v + row * kQ5Stride + 4 * part) = v4f{lo[0], lo[1], lo[2], lo[3]};
+    *(v4f *)(S.v + row * kQ5Stride + 16 + 4 * part) = v4f{hi[0], hi[1], hi[2], hi[3]};
+    if (part == 0) S.d[row] = f16_lut(f.d);
+}
+
+__device__ __forceinline__ float comp(const v4f &v, int k) { return v[k]; }
+
+// Tile (mt, nt) of split sp; blocks [sp * bps, min(G, (sp + 1) * bps)).
+__global__ void __launch_bounds__(256, 4) gemm_q5_kernel(Planes P, const float *__restrict__ x,
+                                                      float *__restrict__ out, int M, int N, int G, int mtiles,
+                                                      int ntiles, int splits, int bps) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
+    Q5Stage *st = (Q5Stage *)lds_raw;
+    // XCD-aware order, as in gemm_kernel: the M-tiles of one weight tile and
+    // split run on one XCD, so the weight tile is read from HBM once into its L2
+    const int total = mtiles * ntiles * splits;
+    const int per_xcd = (total + 7) / 8;
+    const int lin = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (lin >= total) return;
+    const int mt = lin % mtiles;
+    const int rest = lin / mtiles;
+    const int sp = rest % splits, nt = rest / splits;
+    const int m0 = mt * kQ5Tile, n0 = nt * kQ5Tile;
+    const int g0 = sp * bps, g1 = min(G, g0 + bps);
+    const int tn = threadIdx.x & 15, tm = threadIdx.x >> 4;
+
+    float acc[4][4], sum[4][4];
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[r][c] = 0.0f;
+
+    Q5Fetch f;
+    if (g0 < g1) {
+        q5_fetch(P, x, M, N, G, m0, n0, g0, f);
+        q5_store(st[0], f);
+    }
+    __syncthreads();
+    for (int g = g0; g < g1; g++) {
+        const int cur = (g - g0) & 1;
+        if (g + 1 < g1) q5_fetch(P, x, M, N, G, m0, n0, g + 1, f);
+        const Q5Stage &S = st[cur];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) sum[r][c] = 0.0f;
+#pragma unroll 1
+        for (int j0 = 0; j0 < 16; j0 += 4) {
+            // elements j0..j0+3 and 16+j0..: each output's sum still adds its
+            // pairs in increasing j (the order across outputs is free)
+            v4f xa[4], xb[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                xa[r] = *(const v4f *)(S.x + (tm + 16 * r) * kQ5Stride + j0);
+                xb[r] = *(const v4f *)(S.x + (tm + 16 * r) * kQ5Stride + 16 + j0);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const v4f va = *(const v4f *)(S.v + (tn + 16 * c) * kQ5Stride + j0);
+                const v4f vb = *(const v4f *)(S.v + (tn + 16 * c) * kQ5Stride + 16 + j0);
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float p0 = comp(va, k) * comp(xa[r], k);
+                        const float p1 = comp(vb, k) * comp(xb[r], k);
+                        const float pair = p0 + p1;
+                        sum[r][c] = sum[r][c] + pair;
+                    }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float dd = S.d[tn + 16 * c];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float grp = dd * sum[r][c];
+                acc[r][c] = acc[r][c] + grp;
+            }
+        }
+        if (g + 1 < g1) q5_store(st[cur ^ 1], f);
+        __syncthreads();
+    }
+
+    float *o = out + (size_t)sp * M * N;  // splits > 1: partial tile of split sp
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = m0 + tm + 16 * r;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int n = n0 + tn + 16 * c;
+            if (m < M && n < N) o[(size_t)m * N + n] = acc[r][c];
+        }
+    }
+}
+
 // dst = part[0] + part[1] + ... + part[S-1], in split order.
 __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__restrict__ dst, size_t n, int S) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
@@ -351,7 +513,21 @@ struct GemmPlan {
     int wn, splits, sps, mtiles, ntiles;
 };
 
-GemmPlan plan_gemm(int M, int N, int G) {
+GemmPlan plan_gemm_q5(int M, int N, int G) {
+    const int cus = 256;
+    GemmPlan p{};
+    p.wn = 0;
+    p.mtiles = (M + kQ5Tile - 1) / kQ5Tile;
+    p.ntiles = (N + kQ5Tile - 1) / kQ5Tile;
+    int S = 1;
+    while ((int64_t)p.mtiles * p.ntiles * S < 2 * cus && G / (S * 2) >= 4) S *= 2;
+    p.splits = S;
+    p.sps = (G + S - 1) / S;  // blocks per split
+    return p;
+}
+
+GemmPlan plan_gemm(int fmt, int M, int N, int G) {
+    if (fmt == SLLM_Q5_0) return plan_gemm_q5(M, N, G);
     const int cus = 256;
     GemmPlan p{};
     p.mtiles = (M + kBM - 1) / kBM;
@@ -393,13 +569,13 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
 bool gemm_supported(int fmt, int G) {
-    return fmt != SLLM_Q5_0 && G % kKB == 0;
+    return fmt == SLLM_Q5_0 ? G >= 1 : G % kKB == 0;
 }
 
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M) {
-    (void)fmt;
-    const GemmPlan p = plan_gemm(M, N, G);
+    const GemmPlan p = plan_gemm(fmt, M, N, G);
     const size_t parts = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+    if (fmt == SLLM_Q5_0) return align256(parts);
     return align256((size_t)M * G * 32) + 2 * align256((size_t)M * G * 4) + align256(parts);
 }
 
@@ -407,21 +583,31 @@ sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, in
                         size_t ws_bytes, hipStream_t s) {
     if (ws_bytes < gemm_workspace_bytes(fmt, N, G, M)) return set_error(SLLM_ERR_ARG, "gemm: workspace too small");
     if (!gemm_supported(fmt, G)) return set_error(SLLM_ERR_SHAPE, "gemm: format or cols not supported");
-    int8_t *xq = (int8_t *)ws;
-    const size_t q = align256((size_t)M * G * 32), sb = align256((size_t)M * G * 4);
-    float *xsp = (float *)((char *)ws + q);
-    int *sxp = (int *)((char *)ws + q + sb);
-    float *part = (float *)((char *)ws + q + 2 * sb);
-    sllm_status st = launch_quantize_act(x, M, G, xq, xsp, sxp, s);
-    if (st != SLLM_OK) return st;
-    const GemmPlan p = plan_gemm(M, N, G);
-    float *out = p.splits > 1 ? part : dst;
-    switch (fmt) {
-    case SLLM_Q8_0: st = launch_fmt<SLLM_Q8_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-    case SLLM_Q4_0: st = launch_fmt<SLLM_Q4_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-    case SLLM_Q4_1: st = launch_fmt<SLLM_Q4_1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-    case SLLM_Q5K1: st = launch_fmt<SLLM_Q5K1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-    default: return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
+    const GemmPlan p = plan_gemm(fmt, M, N, G);
+    sllm_status st = SLLM_OK;
+    float *part;
+    if (fmt == SLLM_Q5_0) {
+        part = (float *)ws;
+        const int total = p.mtiles * p.ntiles * p.splits;
+        hipLaunchKernelGGL(gemm_q5_kernel, dim3(((total + 7) / 8) * 8), dim3(256), 2 * sizeof(Q5Stage), s, P, x,
+                           p.splits > 1 ? part : dst, M, N, G, p.mtiles, p.ntiles, p.splits, p.sps);
+        SLLM_HIP(hipGetLastError());
+    } else {
+        int8_t *xq = (int8_t *)ws;
+        const size_t q = align256((size_t)M * G * 32), sb = align256((size_t)M * G * 4);
+        float *xsp = (float *)((char *)ws + q);
+        int *sxp = (int *)((char *)ws + q + sb);
+        part = (float *)((char *)ws + q + 2 * sb);
+        st = launch_quantize_act(x, M, G, xq, xsp, sxp, s);
+        if (st != SLLM_OK) return st;
+        float *out = p.splits > 1 ? part : dst;
+        switch (fmt) {
+        case SLLM_Q8_0: st = launch_fmt<SLLM_Q8_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+        case SLLM_Q4_0: st = launch_fmt<SLLM_Q4_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+        case SLLM_Q4_1: st = launch_fmt<SLLM_Q4_1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+        case SLLM_Q5K1: st = launch_fmt<SLLM_Q5K1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
+        default: return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
+        }
     }
     if (st != SLLM_OK || p.splits == 1) return st;
     const size_t n = (size_t)M * N;

@@ -42,7 +42,7 @@ def test_prefill_parity(qtype, M, N, K):
     assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} M={M} {N}x{K}")
 
 
-@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1"])
+@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1", "q5"])
 def test_prefill_edge_activations(qtype):
     # zero rows, denormal rows and huge rows through the GEMM's quantize pre-pass
     N, K, M = 64, 512, 64
@@ -62,7 +62,8 @@ def test_prefill_edge_activations(qtype):
     (13, 4096, 4096, 64),      # C4 Q5_K q/o projection, M = 64
     (13, 1024, 4096, 512),     # C4 Q5_K k/v projection, M = 512
     (12, 14336, 4096, 64),     # C3 Q4_K gate/up, M = 64
-    (6, 4096, 4096, 64),       # C4 Q5_0 (GEMV path)
+    (6, 4096, 4096, 64),       # C4 Q5_0 (VALU GEMM)
+    (6, 1024, 4096, 512),      # C4 Q5_0 k/v, M = 512
 ])
 def test_prefill_full_shapes_on_row_subset(ggml_type, N, K, M):
     raw_gguf = synth.gguf_tensor(ggml_type, 7, N, K)
@@ -89,3 +90,18 @@ def test_gemm_rows_match_gemv_rows():
     one = sq.model_matmul_row_quant_into_f32(w, x[17])
     bound = term_abs_sum("q4_1", raw, N, x[17:18])[0]
     assert np.all(np.abs(big.reshape(64, N)[17].astype(np.float64) - one) <= 2e-5 * bound + 1e-30)
+
+
+@pytest.mark.parametrize("qtype", ["q4_1", "q5"])
+def test_gemm_rows_match_gemv_rows_q5(qtype):
+    # Q5_0's GEMM forms the same per-block fp32 sums as its GEMV (the reference
+    # order); the two may differ only in how the block terms are added up
+    N, K = 192, 1024
+    raw = make_raw(qtype, N, K, seed=8)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    x = make_x(70, K, seed=9)
+    big, _, _ = sq.model_matmul_quant_into_f32(w, x, 70, K)
+    for row in (0, 33, 69):
+        one = sq.model_matmul_row_quant_into_f32(w, x[row])
+        bound = term_abs_sum(qtype, raw, N, x[row:row + 1])[0]
+        assert np.all(np.abs(big.reshape(70, N)[row].astype(np.float64) - one) <= 2e-5 * bound + 1e-30), row
