@@ -346,10 +346,9 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     q, k, v = (torch.empty(n, device="cuda") for n in (H, KV, KV))
     o, gt, up, dn = (torch.empty(n, device="cuda") for n in (H, F, F, H))
     logits = torch.empty(V, device="cuda")
-    sp = stream.cuda_stream
     P = lambda t: t.data_ptr()
 
-    def token():
+    def token(sp):
         for wq, wk, wv, wo, wg, wu, wd in layer_ws:
             sq.matmul_multi_dev([wq, wk, wv], P(xh), 1, H, [P(q), P(k), P(v)], sp)
             sq.matmul_dev(wo, P(xh), 1, H, P(o), sp)
@@ -357,24 +356,42 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             sq.matmul_dev(wd, P(xf), 1, F, P(dn), sp)
         sq.matmul_dev(head, P(xh), 1, H, P(logits), sp)
 
+    def timed(run) -> float:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(tokens):
+            run()
+        b.record(stream)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / tokens
+
     for _ in range(3):
-        token()
+        token(stream.cuda_stream)
     torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record(stream)
-    for _ in range(tokens):
-        token()
-    b.record(stream)
+    ms = timed(lambda: token(stream.cuda_stream))
+    # The same 129 launches captured once in a HIP graph and replayed: the
+    # GEMV path allocates nothing and issues no memset, so it captures as is.
+    ref = logits.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        token(torch.cuda.current_stream().cuda_stream)
+    for _ in range(3):
+        g.replay()
     torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / tokens
-    del layer_ws, head
+    same = bool(torch.equal(logits.view(torch.int32), ref.view(torch.int32)))
+    ms_graph = timed(g.replay)
+    del g, layer_ws, head
     torch.cuda.empty_cache()
     return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
+            "decode_gemv_tok_s_graph": round(1e3 / ms_graph, 1),
+            "decode_gemv_ms_per_token_graph": round(ms_graph, 4),
+            "decode_graph_replay_matches_eager": same,
             "decode_weight_bytes_per_token": tok_bytes,
             "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
-            "decode_note": "129 launches per token (32 layers x [qkv, o, gate+up, down] + head); "
-                           "attention, norms, SwiGLU not included"}
+            "decode_gemv_GBps_graph": round(tok_bytes / (ms_graph * 1e-3) / 1e9, 1),
+            "decode_note": "129 launches per token (32 layers x [qkv, o, gate+up, down] + head), eager on one "
+                           "stream and replayed from one HIP graph; attention, norms, SwiGLU not included"}
 
 
 def cpu_baseline(sq, synth, gate_raw, up_raw, down_raw, copies: int, step_bytes: int,
