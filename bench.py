@@ -59,6 +59,8 @@ def main() -> int:
     ap.add_argument("--decode-tokens", type=int, default=20)
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant GEMV and a 256 MiB copy (for rocprofv3 --pmc runs)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="only launch the prefill GEMMs (C3 / C4 shapes, M = 64 and 512) for rocprofv3 runs")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -79,6 +81,8 @@ def main() -> int:
     H, F = 4096, 14336
     if args.traffic_probe:
         return traffic_probe(sq, synth, torch, stream, args.layers)
+    if args.gemm_probe:
+        return gemm_probe(sq, synth, torch, stream)
     print(f"[bench] building {args.layers} layer copies of C3 weights", file=sys.stderr, flush=True)
     gate_raw = synth.q4k_blocks(100, F, H)
     up_raw = synth.q4k_blocks(101, F, H)
@@ -309,6 +313,32 @@ def traffic_probe(sq, synth, torch, stream, copies: int) -> int:
     torch.cuda.synchronize()
     print(f"traffic probe done: gate+up algorithmic bytes {algo_bytes(list(pairs[0]))}, copy {COPY_BYTES} B",
           flush=True)
+    return 0
+
+
+def gemm_probe(sq, synth, torch, stream) -> int:
+    """Launches for the GEMM profiles: each C3 / C4 prefill shape at M = 64 and
+    512, 10 calls each over 4 rotating weight copies, in a fixed order."""
+    H, F, KV = 4096, 14336, 1024
+    mk = sq.load_weight_f32_direct
+    shapes = [("q4_1 gate", lambda: mk(synth.GGML_Q4_K, synth.q4k_blocks(100, F, H), F, H)),
+              ("q8 down", lambda: mk(synth.GGML_Q6_K, synth.q6k_blocks(102, H, F), H, F)),
+              ("q5k1 q/o", lambda: mk(synth.GGML_Q5_K, synth.q5k_blocks(21, H, H), H, H)),
+              ("q5k1 ffn", lambda: mk(synth.GGML_Q5_K, synth.q5k_blocks(22, F, H), F, H))]
+    wf = synth.normal(30, H * H, 0.02).reshape(H, H)
+    q5raw = synth.quantize_q5_0(wf)
+    shapes.append(("q5 q/o", lambda: sq.DeviceWeight.from_quant(sq.QuantWeight("q5", q5raw, H // 32, H, H))))
+    xs = {c: torch.from_numpy(synth.normal(7, 512 * c)).cuda() for c in (H, F)}
+    y = torch.empty(512 * F, device="cuda")
+    for name, make in shapes:
+        ws = [make() for _ in range(4)]
+        K = ws[0].cols
+        for M in (64, 512):
+            for i in range(10):
+                sq.matmul_dev(ws[i % 4], xs[K].data_ptr(), M, K, y.data_ptr(), stream.cuda_stream)
+            torch.cuda.synchronize()
+            print(f"gemm probe: {name} {ws[0].rows}x{K} M={M} done", flush=True)
+        del ws
     return 0
 
 
