@@ -372,18 +372,21 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     head = mk(14, q6k_head, V, H)
     tok_bytes = sum(w.plane_bytes for ws in layer_ws for w in ws) + head.plane_bytes
     xh = torch.from_numpy(synth.normal(3, H)).cuda()
-    xf = torch.from_numpy(synth.normal(4, F)).cuda()
     q, k, v = (torch.empty(n, device="cuda") for n in (H, KV, KV))
-    o, gt, up, dn = (torch.empty(n, device="cuda") for n in (H, F, F, H))
+    o, dn = (torch.empty(n, device="cuda") for n in (H, H))
     logits = torch.empty(V, device="cuda")
     P = lambda t: t.data_ptr()
 
+    h = torch.empty(F, device="cuda")
+
     def token(sp):
+        # per layer: q/k/v in one launch, o, gate/up + SwiGLU in one launch (h),
+        # down on h; then the head. Attention and norms are not part of this path.
         for wq, wk, wv, wo, wg, wu, wd in layer_ws:
             sq.matmul_multi_dev([wq, wk, wv], P(xh), 1, H, [P(q), P(k), P(v)], sp)
             sq.matmul_dev(wo, P(xh), 1, H, P(o), sp)
-            sq.matmul_multi_dev([wg, wu], P(xh), 1, H, [P(gt), P(up)], sp)
-            sq.matmul_dev(wd, P(xf), 1, F, P(dn), sp)
+            sq.matmul_swiglu_dev(wg, wu, P(xh), 1, H, P(h), 0, 0, sp)
+            sq.matmul_dev(wd, P(h), 1, F, P(dn), sp)
         sq.matmul_dev(head, P(xh), 1, H, P(logits), sp)
 
     def timed(run) -> float:
@@ -402,16 +405,38 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     ms = timed(lambda: token(stream.cuda_stream))
     # The same 129 launches captured once in a HIP graph and replayed: the
     # GEMV path allocates nothing and issues no memset, so it captures as is.
-    ref = logits.clone()
+    ref = (logits.clone(), dn.clone(), h.clone())
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         token(torch.cuda.current_stream().cuda_stream)
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize()
-    same = bool(torch.equal(logits.view(torch.int32), ref.view(torch.int32)))
+    same = all(bool(torch.equal(a.view(torch.int32), b.view(torch.int32))) for a, b in zip((logits, dn, h), ref))
     ms_graph = timed(g.replay)
-    del g, layer_ws, head
+    del g
+
+    # The drop-in path as the Go binding would drive it: host buffers in and
+    # out of every call (x uploaded, dst downloaded, synchronous), with the
+    # host-side multi-weight and SwiGLU entries: 129 calls per token.
+    xh_h = xh.cpu().numpy()
+
+    def token_host():
+        for wq, wk, wv, wo, wg, wu, wd in layer_ws:
+            sq.model_matmul_multi_quant_into_f32([wq, wk, wv], xh_h, 1, H)
+            sq.model_matmul_row_quant_into_f32(wo, xh_h)
+            hh = sq.model_matmul_swiglu_into_f32(wg, wu, xh_h, 1, H)
+            sq.model_matmul_row_quant_into_f32(wd, hh)
+        return sq.model_matmul_row_quant_into_f32(head, xh_h)
+
+    token_host()
+    t0 = time.time()
+    nh = 0
+    while nh < 3 or (time.time() - t0 < 3.0 and nh < tokens):
+        token_host()
+        nh += 1
+    ms_host = (time.time() - t0) / nh * 1e3
+    del layer_ws, head
     torch.cuda.empty_cache()
     return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
             "decode_gemv_tok_s_graph": round(1e3 / ms_graph, 1),
@@ -420,8 +445,11 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             "decode_weight_bytes_per_token": tok_bytes,
             "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
             "decode_gemv_GBps_graph": round(tok_bytes / (ms_graph * 1e-3) / 1e9, 1),
-            "decode_note": "129 launches per token (32 layers x [qkv, o, gate+up, down] + head), eager on one "
-                           "stream and replayed from one HIP graph; attention, norms, SwiGLU not included"}
+            "decode_host_entry_tok_s": round(1e3 / ms_host, 1),
+            "decode_note": "129 launches per token (32 layers x [qkv, o, gate/up+SwiGLU, down] + head), device-"
+                           "resident, eager on one stream and replayed from one HIP graph; decode_host_entry_"
+                           "tok_s: the same 129 calls through the host-buffer entry points (x in, dst out, "
+                           "synchronous, from Python); attention and norms not included"}
 
 
 def cpu_baseline(sq, synth, gate_raw, up_raw, down_raw, copies: int, step_bytes: int,

@@ -148,6 +148,24 @@ sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int c
 sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x_dev, int x_rows,
                                   int x_cols, float *const *dst_dev, void *stream);
 
+/*
+ * forwardBlock's FFN input in one call (model_f32.go:479-490): gate = Wgate x,
+ * up = Wup x (modelMatmulIntoF32 on b.ffnNormed) and then, elementwise,
+ * h = gate * float32(1 / (1 + exp(-float64(gate)))) * up, the reference's
+ * SwiGLU loop in its operation order. h receives x_rows x Rows floats. For
+ * decode (x_rows < 64) and weights of one QType this is a single GEMV launch
+ * that streams each gate row and up row in the same wave and writes h
+ * directly; gate and up are not written unless gate_dev / up_dev are given
+ * (each may be NULL). Wgate and Wup must have the same Rows and Cols == x_cols.
+ */
+sllm_status sllm_matmul_swiglu_dev(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x_dev,
+                                   int x_rows, int x_cols, float *h_dev, float *gate_dev, float *up_dev,
+                                   void *stream);
+
+/* Host-buffer form of sllm_matmul_swiglu_dev (synchronous; h only). */
+sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,
+                                        int x_rows, int x_cols, float *h);
+
 /* argmaxF32 (float32_ops.go:812-822) over n device floats; result to host. */
 sllm_status sllm_argmax_dev(const float *v_dev, int n, int *out, void *stream);
 

@@ -76,6 +76,9 @@ def lib() -> C.CDLL:
         L.ref_argmax.argtypes = [P, i32]
         L.ref_scale_min_k4.argtypes = [i32, P, P, P]
         L.ref_block_bytes.argtypes = [C.c_char_p]
+        L.ref_swiglu.restype = C.c_float
+        L.ref_swiglu.argtypes = [C.c_float, C.c_float]
+        L.ref_swiglu_n.argtypes = [P, P, P, i64]
         _lib = L
     return _lib
 
@@ -195,6 +198,15 @@ def matmul(qtype: str, raw: np.ndarray, N: int, x: np.ndarray) -> np.ndarray:
     if lib().ref_matmul_quant(qtype.encode(), _p(raw), N, K, _p(x), M, _p(dst)):
         raise ValueError(f"unknown qtype {qtype}")
     return dst
+
+
+def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """model_f32.go:486-489 elementwise (libm exp standing in for Go's math.Exp)."""
+    g = np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+    h = np.empty_like(g)
+    lib().ref_swiglu_n(_p(g), _p(u), _p(h), g.size)
+    return h.reshape(np.shape(gate))
 
 
 def argmax(v: np.ndarray) -> int:

@@ -733,3 +733,21 @@ int ref_argmax(const float *v, int n) {
         if (v[i] > bv) { bv = v[i]; best = i; }
     return best;
 }
+
+/* forwardBlock's SwiGLU loop (model_f32.go:486-489):
+ *   g := float64(gateData[i]); s := float32(1.0 / (1.0 + math.Exp(-g)))
+ *   siluData[i] = gateData[i] * s * upData[i]      (float32, left to right)
+ * math.Exp is Go's; libm's exp stands in for it here (both are faithfully
+ * rounded; they can differ in the last bit of the float64, which changes the
+ * float32 s only when that value lies within one float64 ulp of a float32
+ * rounding boundary). */
+float ref_swiglu(float gate, float up) {
+    double e = exp(-(double)gate);
+    float s = (float)(1.0 / (1.0 + e));
+    float t = gate * s;
+    return t * up;
+}
+
+void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n) {
+    for (int64_t i = 0; i < n; i++) h[i] = ref_swiglu(gate[i], up[i]);
+}

@@ -20,6 +20,10 @@
 
 #ifdef __cplusplus
 extern "C" {
+/* model_f32.go:486-489 SwiGLU, one element and n elements. */
+float ref_swiglu(float gate, float up);
+void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
+
 #endif
 
 /* ---- f16 codecs -------------------------------------------------------- */
@@ -100,5 +104,13 @@ int ref_block_bytes(const char *qtype);
 
 #ifdef __cplusplus
 }
+/* model_f32.go:486-489 SwiGLU, one element and n elements. */
+float ref_swiglu(float gate, float up);
+void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
+
 #endif
+/* model_f32.go:486-489 SwiGLU, one element and n elements. */
+float ref_swiglu(float gate, float up);
+void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
+
 #endif

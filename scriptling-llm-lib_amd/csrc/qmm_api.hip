@@ -195,6 +195,19 @@ sllm_status with_upload(const void *host, size_t bytes, size_t extra, F fn) {
     return st;
 }
 
+bool uses_gemm(const sllm_weight *w, int x_rows) {
+    return x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups);
+}
+
+// One weight's matmul on device buffers: the GEMV, or the GEMM with the given
+// activation workspace (at least gemm_workspace_bytes).
+sllm_status run_matmul(const sllm_weight *w, const float *x, int x_rows, float *dst, hipStream_t s, void *ws,
+                       size_t cap) {
+    const Planes P = as_const(w->planes);
+    if (!uses_gemm(w, x_rows)) return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
+}
+
 bool check_shape(int rows, int cols, sllm_status *st) {
     if (rows <= 0 || cols <= 0) {
         *st = set_error(SLLM_ERR_ARG, "rows and cols must be positive");
@@ -424,15 +437,76 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, in
     sllm_status st = ensure_init();
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    Planes P = as_const(w->planes);
-    if (x_rows < tuning().gemm_min_rows || !gemm_supported(w->fmt, w->groups))
-        return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
-    // GEMM: quantized activations go to a per-(device, stream) workspace
-    const size_t need = gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows);
     void *ws = nullptr;
     size_t cap = 0;
-    if ((st = workspace(s, need, &ws, &cap)) != SLLM_OK) return st;
-    return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
+    if (uses_gemm(w, x_rows) && (st = workspace(s, gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows), &ws,
+                                                 &cap)) != SLLM_OK)
+        return st;
+    return run_matmul(w, x, x_rows, dst, s, ws, cap);
+}
+
+sllm_status sllm_matmul_swiglu_dev(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows,
+                                   int x_cols, float *h, float *gate, float *up, void *stream) {
+    if (!wg || !wu || !x || !h) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (wg->cols != x_cols || wu->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match Cols");
+    if (wg->rows != wu->rows) return set_error(SLLM_ERR_ARG, "gate and up have different Rows");
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const int N = wg->rows;
+    if (!uses_gemm(wg, x_rows) && !uses_gemm(wu, x_rows) && wg->fmt == wu->fmt)
+        return launch_gemv_swiglu(wg->fmt, as_const(wg->planes), as_const(wu->planes), x, h, gate, up, N,
+                                  wg->groups, x_rows, s);
+    // Prefill or mixed formats: the two matmuls, then the elementwise SwiGLU.
+    // gate / up land in the caller's buffers or after the GEMM workspace.
+    const size_t mm = (size_t)x_rows * N * sizeof(float);
+    size_t gw = 0;
+    if (uses_gemm(wg, x_rows)) gw = gemm_workspace_bytes(wg->fmt, N, wg->groups, x_rows);
+    if (uses_gemm(wu, x_rows)) {
+        const size_t g2 = gemm_workspace_bytes(wu->fmt, N, wu->groups, x_rows);
+        gw = g2 > gw ? g2 : gw;
+    }
+    gw = (gw + 255) & ~(size_t)255;
+    const size_t extra = (gate ? 0 : ((mm + 255) & ~(size_t)255)) + (up ? 0 : mm);
+    void *ws = nullptr;
+    size_t cap = 0;
+    if (gw + extra > 0 && (st = workspace(s, gw + extra, &ws, &cap)) != SLLM_OK) return st;
+    char *tail = (char *)ws + gw;
+    float *g = gate ? gate : (float *)tail;
+    float *u = up ? up : (float *)(tail + (gate ? 0 : ((mm + 255) & ~(size_t)255)));
+    if ((st = run_matmul(wg, x, x_rows, g, s, ws, gw)) != SLLM_OK) return st;
+    if ((st = run_matmul(wu, x, x_rows, u, s, ws, gw)) != SLLM_OK) return st;
+    return launch_swiglu(g, u, h, (size_t)x_rows * N, s);
+}
+
+sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows,
+                                        int x_cols, float *h) {
+    if (!wg || !wu || !x || !h) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (wg->cols != x_cols || wu->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match Cols");
+    if (wg->rows != wu->rows) return set_error(SLLM_ERR_ARG, "gate and up have different Rows");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    const size_t xb = (size_t)x_rows * x_cols * sizeof(float);
+    const size_t hb = (size_t)x_rows * wg->rows * sizeof(float);
+    const size_t hoff = (xb + 255) & ~(size_t)255;
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, hoff + hb)) != SLLM_OK) return st;
+    float *dx = (float *)c->buf;
+    float *dh = (float *)((char *)c->buf + hoff);
+    hipError_t e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, dh, nullptr, nullptr, c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(h, dh, hb, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "swiglu transfer");
+    return st;
 }
 
 sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int x_rows, int x_cols, float *dst) {
@@ -479,7 +553,7 @@ sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const
     for (int i = 0; i < count; i++) {
         if (done[(size_t)i]) continue;
         const sllm_weight *w = ws[i];
-        if (x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups)) {
+        if (uses_gemm(w, x_rows)) {
             done[(size_t)i] = 1;
             if ((st = sllm_matmul_dev(w, x, x_rows, x_cols, dst[i], stream)) != SLLM_OK) return st;
             continue;

@@ -133,6 +133,19 @@ __device__ __forceinline__ void quantize_part(const float4 *v, int *w, float &sc
     sum = group_sum<TPB>(sm);
 }
 
+// ------------------------------------------------------------- SwiGLU ----
+
+// forwardBlock's FFN activation (model_f32.go:486-489), in its operation order:
+// s = float32(1.0 / (1.0 + exp(-float64(gate)))) in fp64, then (gate * s) * up
+// in fp32. exp is the device's fp64 exp (faithfully rounded), where the
+// reference calls Go's math.Exp.
+__device__ __forceinline__ float swiglu(float gate, float up) {
+    const double e = exp(-(double)gate);
+    const float s = (float)(1.0 / (1.0 + e));
+    const float t = gate * s;
+    return t * up;
+}
+
 // ---------------------------------------------------------- block dots ----
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }

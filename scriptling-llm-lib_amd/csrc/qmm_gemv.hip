@@ -9,16 +9,26 @@
 namespace sllm {
 
 namespace gemv {
-extern template sllm_status launch_mt<SLLM_Q8_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
-                                                 int, int, size_t, hipStream_t);
-extern template sllm_status launch_mt<SLLM_Q4_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
-                                                 int, int, size_t, hipStream_t);
-extern template sllm_status launch_mt<SLLM_Q4_1>(int, int, int, const SegTable &, const float *, int, int, int, int,
-                                                 int, int, size_t, hipStream_t);
-extern template sllm_status launch_mt<SLLM_Q5_0>(int, int, int, const SegTable &, const float *, int, int, int, int,
-                                                 int, int, size_t, hipStream_t);
-extern template sllm_status launch_mt<SLLM_Q5K1>(int, int, int, const SegTable &, const float *, int, int, int, int,
-                                                 int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q8_0, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q8_0, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_0, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_0, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_1, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4_1, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5_0, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5_0, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5K1, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q5K1, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                          int, int, int, size_t, hipStream_t);
 }  // namespace gemv
 
 using namespace gemv;
@@ -42,15 +52,21 @@ int device_cus() {
 
 }  // namespace
 
-sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
-                              const float *x, int G, int M, hipStream_t s) {
+namespace {
+
+// pair: P[0] / P[1] are the gate / up weights of one FFN (N[0] == N[1]) and
+// dst[0..2] receive SwiGLU(gate, up), gate (may be null), up (may be null).
+sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const int *N, int nseg, bool pair,
+                            const float *x, int G, int M, hipStream_t s) {
     if (nseg < 1 || nseg > kMaxSegs) return set_error(SLLM_ERR_ARG, "gemv: 1 to 4 weights per launch");
     if (G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
+    if (pair && (nseg != 2 || N[0] != N[1])) return set_error(SLLM_ERR_ARG, "gemv: gate / up shapes differ");
     int64_t Ntot = 0;
-    for (int i = 0; i < nseg; i++) {
+    for (int i = 0; i < (pair ? 1 : nseg); i++) {
         if (N[i] <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
         Ntot += N[i];
     }
+    const int nrow_segs = pair ? 1 : nseg;  // segments of row waves
     const Tuning &T = tuning();
     const int64_t wgs = (int64_t)device_cus() * T.gemv_wg_per_cu;
     // Rows per wave: the fewest that fit every segment's rows into
@@ -61,7 +77,7 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
     int RPW = (int)((Ntot + slots - 1) / slots);
     auto count_waves = [&](int rpw) {
         int64_t w = 0;
-        for (int i = 0; i < nseg; i++) w += ((int64_t)N[i] + rpw - 1) / rpw;
+        for (int i = 0; i < nrow_segs; i++) w += ((int64_t)N[i] + rpw - 1) / rpw;
         return w;
     };
     while (count_waves(RPW) > slots) RPW++;
@@ -81,7 +97,8 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
         while (NB > 1 && lg % NB) NB--;
         if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
     }
-    while (NB > 1 && RPW * ((lg + NB - 1) / NB) < 4) {
+    const int passes = pair ? 2 : 1;
+    while (NB > 1 && RPW * passes * ((lg + NB - 1) / NB) < 4) {
         int nb = NB - 1;
         while (nb > 1 && lg % nb) nb--;
         NB = nb;
@@ -91,15 +108,15 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
     W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
     const int grid = (int)((waves + W - 1) / W);
     SegTable S{};
-    S.n = nseg;
+    S.n = nrow_segs;
     S.wave0[0] = 0;
     for (int i = 0; i < nseg; i++) {
         S.P[i] = P[i];
         S.N[i] = N[i];
-        S.wave0[i + 1] = S.wave0[i] + (N[i] + RPW - 1) / RPW;
     }
-    S.wave0[nseg] = grid * W;  // the last segment also takes the spare waves
-    const int U = RPW * KCH;
+    for (int i = 0; i < nrow_segs; i++) S.wave0[i + 1] = S.wave0[i] + (N[i] + RPW - 1) / RPW;
+    S.wave0[nrow_segs] = grid * W;  // the last segment also takes the spare waves
+    const int U = RPW * KCH * passes;
     int done = 0;
     while (done < M) {
         const int left = M - done;
@@ -118,20 +135,43 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
         const int mrows = left < MT ? left : MT;
         const size_t lds = act_lds_bytes(fmt, MT, G);
         const float *xp = x + (size_t)done * G * 32;
-        for (int i = 0; i < nseg; i++) S.dst[i] = dst[i] + (size_t)done * N[i];
+        const int ndst = pair ? 3 : nseg;
+        for (int i = 0; i < ndst; i++) {
+            const int rows_i = pair ? N[0] : N[i];  // output i: M x rows_i, rows contiguous per activation row
+            S.dst[i] = dst[i] ? dst[i] + (size_t)done * rows_i : nullptr;
+        }
         sllm_status st;
+#define SLLM_GEMV_FMT(F)                                                                                  \
+    (pair ? launch_mt<F, true>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s)                 \
+          : launch_mt<F, false>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s))
         switch (fmt) {
-        case SLLM_Q8_0: st = launch_mt<SLLM_Q8_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q4_0: st = launch_mt<SLLM_Q4_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q4_1: st = launch_mt<SLLM_Q4_1>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q5_0: st = launch_mt<SLLM_Q5_0>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
-        case SLLM_Q5K1: st = launch_mt<SLLM_Q5K1>(MT, NB, D, S, xp, G, mrows, KCH, RPW, W, grid, lds, s); break;
+        case SLLM_Q8_0: st = SLLM_GEMV_FMT(SLLM_Q8_0); break;
+        case SLLM_Q4_0: st = SLLM_GEMV_FMT(SLLM_Q4_0); break;
+        case SLLM_Q4_1: st = SLLM_GEMV_FMT(SLLM_Q4_1); break;
+        case SLLM_Q5_0: st = SLLM_GEMV_FMT(SLLM_Q5_0); break;
+        case SLLM_Q5K1: st = SLLM_GEMV_FMT(SLLM_Q5K1); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");
         }
+#undef SLLM_GEMV_FMT
         if (st != SLLM_OK) return st;
         done += mrows;
     }
     return SLLM_OK;
+}
+
+}  // namespace
+
+sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
+                              const float *x, int G, int M, hipStream_t s) {
+    return plan_and_launch(fmt, P, dst, N, nseg, false, x, G, M, s);
+}
+
+sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, const float *x, float *h,
+                               float *gate, float *up, int N, int G, int M, hipStream_t s) {
+    const Planes P[2] = {Pg, Pu};
+    float *const dst[3] = {h, gate, up};
+    const int Ns[2] = {N, N};
+    return plan_and_launch(fmt, P, dst, Ns, 2, true, x, G, M, s);
 }
 
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
@@ -272,6 +312,23 @@ sllm_status launch_block_dots(int fmt, const Planes &P, const float *x, int N, i
 
 sllm_status launch_argmax(const float *v, int n, int *out_dev, hipStream_t s) {
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, v, n, out_dev);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+namespace {
+__global__ void swiglu_kernel(const float *__restrict__ gate, const float *__restrict__ up, float *__restrict__ h,
+                              size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        h[i] = swiglu(gate[i], up[i]);
+}
+}  // namespace
+
+sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s) {
+    if (n == 0) return SLLM_OK;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, gate, up,
+                       h, n);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

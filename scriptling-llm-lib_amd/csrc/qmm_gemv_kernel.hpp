@@ -211,9 +211,9 @@ __device__ __forceinline__ float wave_sum(float v) {
     return ((r0 + r1) + r2) + r3;
 }
 
-template <int FMT, int NB, int D, int TPB, class NextBase>
-__device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB], const float *__restrict__ x,
-                                         int M, int G, const ActView &A, NextBase &next_base) {
+template <int FMT, int NB, int D, int TPB, class Issue>
+__device__ __forceinline__ void prologue(BlockRegs (&buf)[D][NB], const float *__restrict__ x, int M, int G,
+                                         const ActView &A, Issue &issue) {
     constexpr int NV = 8 / TPB;  // float4 per thread per block
     const int nblk = M * G;
     const int per_pass = blockDim.x / TPB;
@@ -225,12 +225,12 @@ __device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB
         for (int k = 0; k < NV; k++) xv[k] = src[k];
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
+        for (int d = 0; d < D; d++) issue(buf[d]);
         __builtin_amdgcn_sched_barrier(0);
         stage_part<FMT, TPB>(xv, blk, sub, A);
     } else {
 #pragma unroll
-        for (int d = 0; d < D; d++) load_unit<FMT, NB>(P, buf[d], next_base());
+        for (int d = 0; d < D; d++) issue(buf[d]);
     }
     for (int b = blk + per_pass; b < nblk; b += per_pass) {
         float4 v[NV];
@@ -244,6 +244,9 @@ __device__ __forceinline__ void prologue(const Planes &P, BlockRegs (&buf)[D][NB
 // The weights of one launch (same format, same K, same activation rows).
 // Segment s owns the waves [wave0[s], wave0[s + 1]) of the grid; wave0[n] is
 // the grid's wave count, so the last segment also takes the spare waves.
+// Paired launch (gate / up of one FFN): a single segment of row waves; P[1]
+// holds the up planes, dst[0] receives SwiGLU(gate, up), dst[1] / dst[2]
+// (optional) the gate / up outputs themselves.
 struct SegTable {
     Planes P[kMaxSegs];
     float *dst[kMaxSegs];
@@ -256,8 +259,9 @@ struct SegTable {
 // number (t / KCH), rows being wv, wv + TW, ... of its segment's weight (at
 // most RPW of them). A unit is NB blocks per lane. The wave keeps D units in
 // flight in a register ring: it computes unit t, then issues the loads of
-// unit t + D into the registers it just consumed.
-template <int FMT, int NB, int D, int MT, bool HOIST>
+// unit t + D into the registers it just consumed. PAIR: each row is streamed
+// twice, gate chunks then up chunks, and the wave combines the two sums.
+template <int FMT, int NB, int D, int MT, bool HOIST, bool PAIR>
 __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__restrict__ x, int G, int M,
                                                     int KCH, int RPW, int tpb) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -279,30 +283,43 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
             w1 = S.wave0[s + 1];
         }
     }
+    const Planes P2 = S.P[PAIR ? 1 : 0];  // PAIR: the up planes
     const int TW = w1 - w0;
     const int wv = wg - w0;
-    const int U = RPW * KCH;
+    constexpr int PH = PAIR ? 2 : 1;  // passes over each row
+    const int U = RPW * KCH * PH;
     constexpr int CH = 64 * NB;  // blocks per K-chunk
 
-    // Load-stream position (row ordinal lq, chunk lk). Every wave runs U units;
-    // one with fewer than RPW rows re-reads its last real unit for the rest
-    // (the data is still in flight or in cache, and no two waves pile onto the
-    // same lines); those rows' sums land in lanes whose row is >= N and are
-    // not stored.
+    // Load-stream position (row ordinal lq, chunk lk, pass lp). Every wave runs
+    // U units; one with fewer than RPW rows re-reads its last real unit for the
+    // rest (the data is still in flight or in cache, and no two waves pile
+    // onto the same lines); those rows' sums land in lanes whose row is >= N
+    // and are not stored.
     const int real_rows = wv < N ? (N - 1 - wv) / TW + 1 : 0;
-    const int U_real = real_rows * KCH;
-    int lq = 0, lk = 0, lt = 0;
+    const int U_real = real_rows * KCH * PH;
+    int lq = 0, lk = 0, lp = 0, lt = 0;
+    bool lup = false;  // the unit last issued reads the up planes
     uint32_t last = (uint32_t)min(wv, N - 1) * (uint32_t)G + (uint32_t)lane;
     auto next_base = [&]() -> uint32_t {
         if (lt >= U_real) return last;
         const int row = wv + lq * TW;
         last = (uint32_t)row * (uint32_t)G + (uint32_t)(lk * CH + lane);
+        lup = PAIR && lp == 1;
         ++lt;
         if (++lk == KCH) {
             lk = 0;
-            ++lq;
+            if (PAIR && lp == 0) {
+                lp = 1;
+            } else {
+                lp = 0;
+                ++lq;
+            }
         }
         return last;
+    };
+    auto issue = [&](BlockRegs (&u)[NB]) {
+        const uint32_t base = next_base();
+        load_unit<FMT, NB>(lup ? P2 : P, u, base);
     };
 
     BlockRegs buf[D][NB];
@@ -311,17 +328,20 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     // then its wave's first D units of weights, then quantizes: it waits only
     // for its activation loads while the weight stream is in flight.
     switch (tpb) {
-    case 8: prologue<FMT, NB, D, 8>(P, buf, x, M, G, A, next_base); break;
-    case 4: prologue<FMT, NB, D, 4>(P, buf, x, M, G, A, next_base); break;
-    case 2: prologue<FMT, NB, D, 2>(P, buf, x, M, G, A, next_base); break;
-    default: prologue<FMT, NB, D, 1>(P, buf, x, M, G, A, next_base); break;
+    case 8: prologue<FMT, NB, D, 8>(buf, x, M, G, A, issue); break;
+    case 4: prologue<FMT, NB, D, 4>(buf, x, M, G, A, issue); break;
+    case 2: prologue<FMT, NB, D, 2>(buf, x, M, G, A, issue); break;
+    default: prologue<FMT, NB, D, 1>(buf, x, M, G, A, issue); break;
     }
     __syncthreads();
 
-    float acc[MT], acc2[MT], res[MT];
+    float acc[MT], acc2[MT], res[MT], resg[PAIR ? MT : 1];
 #pragma unroll
-    for (int m = 0; m < MT; m++) acc[m] = acc2[m] = res[m] = 0.0f;
-    int cq = 0, ck = 0;  // compute-stream position
+    for (int m = 0; m < MT; m++) {
+        acc[m] = acc2[m] = res[m] = 0.0f;
+        resg[PAIR ? m : 0] = 0.0f;
+    }
+    int cq = 0, ck = 0, cp = 0;  // compute-stream position (row ordinal, chunk, pass)
 
     // HOIST (a row is one K-chunk): every unit uses the same blocks, so the
     // activation operands are read from LDS once, before the loop.
@@ -363,15 +383,22 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
         }
         if (++ck == KCH) {
             // row done: reduce across the wave (fixed order), park it in lane cq
+            // (PAIR: the gate pass in resg, the up pass in res)
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 float v = wave_sum(acc[m]);
                 if (FMT == SLLM_Q5K1) v = v + wave_sum(acc2[m]);
-                res[m] = (lane == cq) ? v : res[m];
+                if (PAIR && cp == 0) resg[PAIR ? m : 0] = (lane == cq) ? v : resg[PAIR ? m : 0];
+                else res[m] = (lane == cq) ? v : res[m];
                 acc[m] = acc2[m] = 0.0f;
             }
             ck = 0;
-            ++cq;
+            if (PAIR && cp == 0) {
+                cp = 1;
+            } else {
+                cp = 0;
+                ++cq;
+            }
         }
     };
 
@@ -384,14 +411,14 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
 #pragma unroll
         for (int d = 0; d < D; d++) {
             compute(buf[d]);
-            load_unit<FMT, NB>(P, buf[d], next_base());
+            issue(buf[d]);
         }
     }
     const int rem = U - t0 - D;
 #pragma unroll
     for (int d = 0; d < D; d++) {
         compute(buf[d]);
-        if (d < rem) load_unit<FMT, NB>(P, buf[d], next_base());
+        if (d < rem) issue(buf[d]);
     }
 #pragma unroll
     for (int d = 0; d < D; d++)
@@ -400,12 +427,22 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     const int row = wv + lane * TW;
     if (lane < RPW && row < N) {
 #pragma unroll
-        for (int m = 0; m < MT; m++)
-            if (m < M) dst[(size_t)m * N + row] = res[m];
+        for (int m = 0; m < MT; m++) {
+            if (m >= M) continue;
+            const size_t o = (size_t)m * N + row;
+            if (PAIR) {
+                const float g = resg[PAIR ? m : 0], u = res[m];
+                dst[o] = swiglu(g, u);
+                if (S.dst[1]) S.dst[1][o] = g;
+                if (S.dst[2]) S.dst[2][o] = u;
+            } else {
+                dst[o] = res[m];
+            }
+        }
     }
 }
 
-template <int FMT, int NB, int D, int MT>
+template <int FMT, int NB, int D, int MT, bool PAIR>
 sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
                      size_t lds, hipStream_t s) {
     // hoisting needs room for the operands: not for Q5_0 (32 fp32 per block)
@@ -414,49 +451,49 @@ sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, i
     int tpb = 8;
     while (tpb > 1 && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
     if (kCanHoist && KCH == 1)
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M,
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist, PAIR>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M,
                            KCH, RPW, tpb);
     else
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M, KCH,
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false, PAIR>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M, KCH,
                            RPW, tpb);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }
 
 // D units in flight; NB * D * MT <= 8 blocks per lane.
-template <int FMT, int NB, int MT>
+template <int FMT, int NB, int MT, bool PAIR>
 sllm_status launch_d(int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
                      size_t lds, hipStream_t s) {
     constexpr int DMAX = 8 / (NB * MT) >= 8 ? 8 : (8 / (NB * MT) >= 4 ? 4 : (8 / (NB * MT) >= 2 ? 2 : 1));
-    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
-    return launch_t<FMT, NB, 1, MT>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 8 && DMAX >= 8) return launch_t<FMT, NB, (DMAX >= 8 ? 8 : 1), MT, PAIR>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 4 && DMAX >= 4) return launch_t<FMT, NB, (DMAX >= 4 ? 4 : 1), MT, PAIR>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    if (D >= 2 && DMAX >= 2) return launch_t<FMT, NB, (DMAX >= 2 ? 2 : 1), MT, PAIR>(S, x, G, M, KCH, RPW, W, grid, lds, s);
+    return launch_t<FMT, NB, 1, MT, PAIR>(S, x, G, M, KCH, RPW, W, grid, lds, s);
 }
 
-template <int FMT, int MT>
+template <int FMT, int MT, bool PAIR>
 sllm_status launch_nb(int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W,
                       int grid, size_t lds, hipStream_t s) {
     switch (NB) {
-    case 1: return launch_d<FMT, 1, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_d<FMT, 2, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 3: return launch_d<FMT, 3, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_d<FMT, 4, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 5: return launch_d<FMT, 5, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 6: return launch_d<FMT, 6, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 7: return launch_d<FMT, 7, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 8: return launch_d<FMT, 8, MT>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 1: return launch_d<FMT, 1, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_d<FMT, 2, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 3: return launch_d<FMT, 3, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_d<FMT, 4, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 5: return launch_d<FMT, 5, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 6: return launch_d<FMT, 6, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 7: return launch_d<FMT, 7, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 8: return launch_d<FMT, 8, MT, PAIR>(D, S, x, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported blocks-per-lane");
 }
 
-template <int FMT>
+template <int FMT, bool PAIR>
 sllm_status launch_mt(int MT, int NB, int D, const SegTable &S, const float *x, int G, int M, int KCH, int RPW,
                       int W, int grid, size_t lds, hipStream_t s) {
     switch (MT) {
-    case 1: return launch_nb<FMT, 1>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 2: return launch_nb<FMT, 2>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
-    case 4: return launch_nb<FMT, 4>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 1: return launch_nb<FMT, 1, PAIR>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 2: return launch_nb<FMT, 2, PAIR>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
+    case 4: return launch_nb<FMT, 4, PAIR>(NB, D, S, x, G, M, KCH, RPW, W, grid, lds, s);
     }
     return set_error(SLLM_ERR_SHAPE, "gemv: unsupported row tile");
 }

@@ -94,6 +94,13 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
 constexpr int kMaxSegs = 4;
 sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
                               const float *x, int G, int M, hipStream_t s);
+// Paired gate / up GEMV of one FFN: h = SwiGLU(Wg x, Wu x) (model_f32.go:479-490);
+// gate / up (may be null) also receive the two matmul outputs. Both weights
+// have the same format, N rows and G blocks per row.
+sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, const float *x, float *h,
+                               float *gate, float *up, int N, int G, int M, hipStream_t s);
+// h[i] = SwiGLU(gate[i], up[i]) for n elements (the prefill path and mixed formats).
+sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s);
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         void *ws, size_t ws_bytes, hipStream_t s);
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M);

@@ -81,6 +81,8 @@ def lib() -> C.CDLL:
     L.sllm_matmul_dev.argtypes = [W, P, i32, i32, P, P]
     L.sllm_matmul_multi_quant_into_f32.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P)]
     L.sllm_matmul_multi_dev.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P), P]
+    L.sllm_matmul_swiglu_dev.argtypes = [W, W, P, i32, i32, P, P, P, P]
+    L.sllm_matmul_swiglu_into_f32.argtypes = [W, W, P, i32, i32, P]
     L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
     L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
@@ -260,6 +262,26 @@ def matmul_multi_dev(ws: list, x_ptr: int, x_rows: int, x_cols: int, dst_ptrs: l
     hs = (C.c_void_p * len(ws))(*[w.handle for w in ws])
     ds = (C.c_void_p * len(ws))(*[C.c_void_p(p) for p in dst_ptrs])
     _check(lib().sllm_matmul_multi_dev(hs, len(ws), C.c_void_p(x_ptr), x_rows, x_cols, ds, C.c_void_p(stream)))
+
+
+def model_matmul_swiglu_into_f32(w_gate: DeviceWeight, w_up: DeviceWeight, x_data: np.ndarray, x_rows: int,
+                                 x_cols: int) -> np.ndarray:
+    """forwardBlock's gate / up matmuls and SwiGLU loop (model_f32.go:479-490) in
+    one call: returns h (x_rows * Rows float32)."""
+    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    if x.size < x_rows * x_cols:
+        raise SllmError(1, "xData shorter than xRows*xCols")
+    h = np.empty(x_rows * w_gate.rows, np.float32)
+    _check(lib().sllm_matmul_swiglu_into_f32(w_gate.handle, w_up.handle, _ptr(x), x_rows, x_cols, _ptr(h)))
+    return h
+
+
+def matmul_swiglu_dev(w_gate: DeviceWeight, w_up: DeviceWeight, x_ptr: int, x_rows: int, x_cols: int, h_ptr: int,
+                      gate_ptr: int = 0, up_ptr: int = 0, stream: int = 0) -> None:
+    """Device-resident gate / up matmuls + SwiGLU (gate / up outputs optional)."""
+    _check(lib().sllm_matmul_swiglu_dev(w_gate.handle, w_up.handle, C.c_void_p(x_ptr), x_rows, x_cols,
+                                        C.c_void_p(h_ptr), C.c_void_p(gate_ptr or None),
+                                        C.c_void_p(up_ptr or None), C.c_void_p(stream)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

@@ -51,6 +51,8 @@ def test_argument_errors_need_no_device():
     ds = (C.c_void_p * 1)(p)
     assert lib.sllm_matmul_multi_quant_into_f32(hs, 0, p, 1, 32, ds) == 1                 # count 0
     assert lib.sllm_matmul_multi_dev(hs, 1, p, 1, 32, ds, None) == 1                        # null weight
+    assert lib.sllm_matmul_swiglu_dev(None, None, p, 1, 32, p, None, None, None) == 1      # null weights
+    assert lib.sllm_matmul_swiglu_into_f32(None, None, p, 1, 32, p) == 1
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
@@ -70,5 +72,5 @@ def test_python_host_mirror_names():
     # the Go entry points this path replaces, mirrored by the host module
     for name in ("QuantWeight", "load_weight_f32_direct", "quantize_q8_rows_f32",
                  "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev",
-                 "model_matmul_multi_quant_into_f32"):
+                 "model_matmul_multi_quant_into_f32", "model_matmul_swiglu_into_f32"):
         assert hasattr(sq, name)
