@@ -374,7 +374,7 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     xh = torch.from_numpy(synth.normal(3, H)).cuda()
     q, k, v = (torch.empty(n, device="cuda") for n in (H, KV, KV))
     o, dn = (torch.empty(n, device="cuda") for n in (H, H))
-    logits = torch.empty(V, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
     P = lambda t: t.data_ptr()
 
     h = torch.empty(F, device="cuda")
@@ -387,7 +387,7 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             sq.matmul_dev(wo, P(xh), 1, H, P(o), sp)
             sq.matmul_swiglu_dev(wg, wu, P(xh), 1, H, P(h), 0, 0, sp)
             sq.matmul_dev(wd, P(h), 1, F, P(dn), sp)
-        sq.matmul_dev(head, P(xh), 1, H, P(logits), sp)
+        sq.matmul_argmax_dev(head, P(xh), P(tok), 0, sp)  # head + greedy argmax, one launch
 
     def timed(run) -> float:
         a = torch.cuda.Event(enable_timing=True)
@@ -405,14 +405,18 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     ms = timed(lambda: token(stream.cuda_stream))
     # The same 129 launches captured once in a HIP graph and replayed: the
     # GEMV path allocates nothing and issues no memset, so it captures as is.
-    ref = (logits.clone(), dn.clone(), h.clone())
+    ref = (tok.clone(), dn.clone(), h.clone())
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        token(cs.cuda_stream)  # first use of cs allocates its argmax scratch: before capture
+    cs.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        token(torch.cuda.current_stream().cuda_stream)
+    with torch.cuda.graph(g, stream=cs):
+        token(cs.cuda_stream)
     for _ in range(3):
         g.replay()
     torch.cuda.synchronize()
-    same = all(bool(torch.equal(a.view(torch.int32), b.view(torch.int32))) for a, b in zip((logits, dn, h), ref))
+    same = all(bool(torch.equal(a.view(torch.int32), b.view(torch.int32))) for a, b in zip((tok, dn, h), ref))
     ms_graph = timed(g.replay)
     del g
 
@@ -427,7 +431,7 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             sq.model_matmul_row_quant_into_f32(wo, xh_h)
             hh = sq.model_matmul_swiglu_into_f32(wg, wu, xh_h, 1, H)
             sq.model_matmul_row_quant_into_f32(wd, hh)
-        return sq.model_matmul_row_quant_into_f32(head, xh_h)
+        return sq.matmul_argmax(head, xh_h)
 
     token_host()
     t0 = time.time()
@@ -446,8 +450,9 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
             "decode_gemv_GBps_graph": round(tok_bytes / (ms_graph * 1e-3) / 1e9, 1),
             "decode_host_entry_tok_s": round(1e3 / ms_host, 1),
-            "decode_note": "129 launches per token (32 layers x [qkv, o, gate/up+SwiGLU, down] + head), device-"
-                           "resident, eager on one stream and replayed from one HIP graph; decode_host_entry_"
+            "decode_note": "129 launches per token (32 layers x [qkv, o, gate/up+SwiGLU, down] + head with greedy "
+                           "argmax), device-resident, eager on one stream and replayed from one HIP graph; "
+                           "decode_host_entry_"
                            "tok_s: the same 129 calls through the host-buffer entry points (x in, dst out, "
                            "synchronous, from Python); attention and norms not included"}
 

@@ -166,6 +166,21 @@ sllm_status sllm_matmul_swiglu_dev(const sllm_weight *w_gate, const sllm_weight 
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,
                                         int x_rows, int x_cols, float *h);
 
+/*
+ * The output head and greedy sampling in one launch: modelMatmulRowQuantIntoF32
+ * of one activation row (outputLogits, model_f32.go:521) followed by argmaxF32
+ * (float32_ops.go:812-822) of the logits: the first index of the maximum, NaN
+ * values never winning, and 0 if logits[0] is NaN. *argmax_dev (device int)
+ * receives the index; logits_dev (may be NULL) the logits. Needs
+ * x_cols == Cols. Launches on the same stream are serialized; launches on
+ * different streams each use their own 64-byte scratch.
+ */
+sllm_status sllm_matmul_argmax_dev(const sllm_weight *w, const float *x_dev, int x_cols, float *logits_dev,
+                                   int *argmax_dev, void *stream);
+
+/* Host-buffer form: normed in, the greedy token out (4 bytes read back, not the logits). */
+sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *token);
+
 /* argmaxF32 (float32_ops.go:812-822) over n device floats; result to host. */
 sllm_status sllm_argmax_dev(const float *v_dev, int n, int *out, void *stream);
 

@@ -48,6 +48,31 @@ struct Ws {
 };
 std::unordered_map<uint64_t, Ws> g_ws;
 
+// Argmax scratch per (device, stream): a 64-bit key and two counters, zeroed
+// once at allocation; every argmax launch leaves them zeroed again.
+std::unordered_map<uint64_t, void *> g_amax;
+
+sllm_status amax_scratch(hipStream_t stream, void **out) {
+    int dev = 0;
+    SLLM_HIP(hipGetDevice(&dev));
+    const uint64_t key = ((uint64_t)(uintptr_t)stream << 8) ^ (uint64_t)dev;
+    std::lock_guard<std::mutex> lk(g_mu);
+    void *&p = g_amax[key];
+    if (!p) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return set_error(SLLM_ERR_ARG, "argmax: the first call on a stream allocates its scratch; "
+                                           "make one call on the stream before capturing it");
+        if (hipMalloc(&p, 64) != hipSuccess) {
+            p = nullptr;
+            return set_error(SLLM_ERR_OOM, "argmax scratch allocation failed");
+        }
+        SLLM_HIP(hipMemset(p, 0, 64));
+    }
+    *out = p;
+    return SLLM_OK;
+}
+
 // The GEMM activation workspace of `stream` on the current device, grown to at
 // least `need` bytes. Growing synchronizes the stream before freeing the old
 // buffer (work already queued on it may still read it).
@@ -443,6 +468,43 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, in
                                                  &cap)) != SLLM_OK)
         return st;
     return run_matmul(w, x, x_rows, dst, s, ws, cap);
+}
+
+sllm_status sllm_matmul_argmax_dev(const sllm_weight *w, const float *x, int x_cols, float *logits, int *argmax,
+                                   void *stream) {
+    if (!w || !x || !argmax) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_cols != w->cols) return set_error(SLLM_ERR_ARG, "xCols does not match the weight's Cols");
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    void *scr = nullptr;
+    if ((st = amax_scratch(s, &scr)) != SLLM_OK) return st;
+    return launch_gemv_argmax(w->fmt, as_const(w->planes), x, logits, w->rows, w->groups,
+                              (unsigned long long *)scr, (unsigned int *)((char *)scr + 8), argmax, s);
+}
+
+sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *token) {
+    if (!w || !normed || !token) return set_error(SLLM_ERR_ARG, "null pointer");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    const size_t xb = (size_t)w->cols * sizeof(float);
+    const size_t ooff = (xb + 255) & ~(size_t)255;
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, ooff + 256)) != SLLM_OK) return st;
+    float *dx = (float *)c->buf;
+    int *dout = (int *)((char *)c->buf + ooff);
+    hipError_t e = hipMemcpyAsync(dx, normed, xb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, dout, c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(token, dout, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "argmax transfer");
+    return st;
 }
 
 sllm_status sllm_matmul_swiglu_dev(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows,

@@ -57,7 +57,8 @@ namespace {
 // pair: P[0] / P[1] are the gate / up weights of one FFN (N[0] == N[1]) and
 // dst[0..2] receive SwiGLU(gate, up), gate (may be null), up (may be null).
 sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const int *N, int nseg, bool pair,
-                            const float *x, int G, int M, hipStream_t s) {
+                            const float *x, int G, int M, hipStream_t s, unsigned long long *amax_key = nullptr,
+                            unsigned int *amax_cnt = nullptr, int *amax_out = nullptr) {
     if (nseg < 1 || nseg > kMaxSegs) return set_error(SLLM_ERR_ARG, "gemv: 1 to 4 weights per launch");
     if (G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
     if (pair && (nseg != 2 || N[0] != N[1])) return set_error(SLLM_ERR_ARG, "gemv: gate / up shapes differ");
@@ -107,8 +108,12 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     int W = (int)((waves + wgs - 1) / wgs);
     W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
     const int grid = (int)((waves + W - 1) / W);
+    if (amax_key && (M != 1 || nseg != 1 || pair)) return set_error(SLLM_ERR_ARG, "gemv: argmax needs one row");
     SegTable S{};
     S.n = nrow_segs;
+    S.amax_key = amax_key;
+    S.amax_cnt = amax_cnt;
+    S.amax_out = amax_out;
     S.wave0[0] = 0;
     for (int i = 0; i < nseg; i++) {
         S.P[i] = P[i];
@@ -177,6 +182,11 @@ sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, cons
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         hipStream_t s) {
     return launch_gemv_multi(fmt, &P, &dst, &N, 1, x, G, M, s);
+}
+
+sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
+                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s) {
+    return plan_and_launch(fmt, &P, &logits, &N, 1, false, x, G, 1, s, key, cnt, out);
 }
 
 // ------------------------------------------------------ verification ----

@@ -247,13 +247,63 @@ __device__ __forceinline__ void prologue(BlockRegs (&buf)[D][NB], const float *_
 // Paired launch (gate / up of one FFN): a single segment of row waves; P[1]
 // holds the up planes, dst[0] receives SwiGLU(gate, up), dst[1] / dst[2]
 // (optional) the gate / up outputs themselves.
+// Greedy argmax of a one-row, one-weight launch (argmaxF32, float32_ops.go:
+// 812-822): amax_key != null turns it on. key / cnt are per-stream scratch
+// that every launch leaves at zero; out receives the index.
 struct SegTable {
     Planes P[kMaxSegs];
     float *dst[kMaxSegs];
     int N[kMaxSegs];
     int wave0[kMaxSegs + 1];
     int n;
+    unsigned long long *amax_key;
+    unsigned int *amax_cnt;  // [0] workgroups done, [1] row 0 is NaN
+    int *amax_out;
 };
+
+// Order-preserving key of a non-NaN value and its row: larger values give
+// larger keys, and among equal values the lowest row the largest (the first
+// maximum wins, as with the reference's strict `>`). -0 and +0 are equal.
+__device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
+    uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((unsigned long long)u << 32) | (uint32_t)~(uint32_t)row;
+}
+
+// Argmax over the launch's outputs: each wave takes the largest key of its
+// rows (NaN rows never win), the workgroup's waves meet in LDS, one atomic
+// max per workgroup; the last workgroup to finish writes the index and
+// clears the scratch for the next launch. If row 0 is NaN the answer is 0
+// (no value compares greater than the reference's starting NaN).
+__device__ __forceinline__ void argmax_tail(const SegTable &S, float v, bool mine, int row) {
+    __shared__ unsigned long long slot[16];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    unsigned long long k = (mine && !__builtin_isnan(v)) ? argmax_key(v, row) : 0ull;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const unsigned long long o = __shfl_xor(k, off, 64);
+        k = o > k ? o : k;
+    }
+    if (mine && row == 0 && __builtin_isnan(v)) atomicOr(&S.amax_cnt[1], 1u);
+    if (lane == 0) slot[wave] = k;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long best = 0;
+        for (int w = 0; w < W; w++) best = slot[w] > best ? slot[w] : best;
+        if (best) atomicMax(S.amax_key, best);
+        __threadfence();
+        if (atomicAdd(&S.amax_cnt[0], 1u) == gridDim.x - 1) {
+            __threadfence();
+            const unsigned long long fin = atomicAdd(S.amax_key, 0ull);
+            const unsigned int nan0 = atomicAdd(&S.amax_cnt[1], 0u);
+            *S.amax_out = (nan0 || fin == 0) ? 0 : (int)~(uint32_t)fin;
+            atomicExch(S.amax_key, 0ull);
+            atomicExch(&S.amax_cnt[1], 0u);
+            __threadfence();
+            atomicExch(&S.amax_cnt[0], 0u);
+        }
+    }
+}
 
 // A wave's work is a stream of units: unit t is K-chunk (t % KCH) of its row
 // number (t / KCH), rows being wv, wv + TW, ... of its segment's weight (at
@@ -435,11 +485,12 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
                 dst[o] = swiglu(g, u);
                 if (S.dst[1]) S.dst[1][o] = g;
                 if (S.dst[2]) S.dst[2][o] = u;
-            } else {
+            } else if (dst) {
                 dst[o] = res[m];
             }
         }
     }
+    if (!PAIR && S.amax_key) argmax_tail(S, res[0], lane < RPW && row < N, row);
 }
 
 template <int FMT, int NB, int D, int MT, bool PAIR>

@@ -99,6 +99,11 @@ sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const
 // have the same format, N rows and G blocks per row.
 sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, const float *x, float *h,
                                float *gate, float *up, int N, int G, int M, hipStream_t s);
+// One-row GEMV that also writes the greedy argmax of its outputs to *out
+// (device). logits may be null. key / cnt: 16 bytes of zeroed per-stream
+// scratch, left zeroed again by every launch.
+sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
+                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s);
 // h[i] = SwiGLU(gate[i], up[i]) for n elements (the prefill path and mixed formats).
 sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s);
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,

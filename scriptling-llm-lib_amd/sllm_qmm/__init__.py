@@ -82,6 +82,8 @@ def lib() -> C.CDLL:
     L.sllm_matmul_multi_quant_into_f32.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P)]
     L.sllm_matmul_multi_dev.argtypes = [C.POINTER(W), i32, P, i32, i32, C.POINTER(P), P]
     L.sllm_matmul_swiglu_dev.argtypes = [W, W, P, i32, i32, P, P, P, P]
+    L.sllm_matmul_argmax_dev.argtypes = [W, P, i32, P, P, P]
+    L.sllm_matmul_argmax.argtypes = [W, P, C.POINTER(i32)]
     L.sllm_matmul_swiglu_into_f32.argtypes = [W, W, P, i32, i32, P]
     L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
@@ -282,6 +284,23 @@ def matmul_swiglu_dev(w_gate: DeviceWeight, w_up: DeviceWeight, x_ptr: int, x_ro
     _check(lib().sllm_matmul_swiglu_dev(w_gate.handle, w_up.handle, C.c_void_p(x_ptr), x_rows, x_cols,
                                         C.c_void_p(h_ptr), C.c_void_p(gate_ptr or None),
                                         C.c_void_p(up_ptr or None), C.c_void_p(stream)))
+
+
+def matmul_argmax(w: DeviceWeight, normed: np.ndarray) -> int:
+    """outputLogits' head matmul + argmaxF32 (greedy token) in one launch; only
+    the index comes back to the host."""
+    x = np.ascontiguousarray(normed, dtype=np.float32).reshape(-1)
+    if x.size < w.cols:
+        raise SllmError(1, "normed shorter than Cols")
+    out = C.c_int()
+    _check(lib().sllm_matmul_argmax(w.handle, _ptr(x), C.byref(out)))
+    return out.value
+
+
+def matmul_argmax_dev(w: DeviceWeight, x_ptr: int, argmax_ptr: int, logits_ptr: int = 0, stream: int = 0) -> None:
+    """Device-resident head matmul + argmax: *argmax_ptr (device int32) gets the index."""
+    _check(lib().sllm_matmul_argmax_dev(w.handle, C.c_void_p(x_ptr), w.cols, C.c_void_p(logits_ptr or None),
+                                        C.c_void_p(argmax_ptr), C.c_void_p(stream)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

@@ -53,6 +53,8 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_matmul_multi_dev(hs, 1, p, 1, 32, ds, None) == 1                        # null weight
     assert lib.sllm_matmul_swiglu_dev(None, None, p, 1, 32, p, None, None, None) == 1      # null weights
     assert lib.sllm_matmul_swiglu_into_f32(None, None, p, 1, 32, p) == 1
+    assert lib.sllm_matmul_argmax(None, p, C.byref(C.c_int())) == 1
+    assert lib.sllm_matmul_argmax_dev(None, p, 32, None, p, None) == 1
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
@@ -72,5 +74,5 @@ def test_python_host_mirror_names():
     # the Go entry points this path replaces, mirrored by the host module
     for name in ("QuantWeight", "load_weight_f32_direct", "quantize_q8_rows_f32",
                  "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev",
-                 "model_matmul_multi_quant_into_f32", "model_matmul_swiglu_into_f32"):
+                 "model_matmul_multi_quant_into_f32", "model_matmul_swiglu_into_f32", "matmul_argmax"):
         assert hasattr(sq, name)
