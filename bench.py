@@ -352,10 +352,13 @@ def load_traffic() -> dict | None:
 
 
 def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
-    """All linears of one decode token of a 32-layer Q4_K_M Llama-3-8B shape + Q6_K head.
+    """All linears of one decode token of a 32-layer Q4_K_M Llama-3-8B shape + Q6_K head,
+    with the RMSNorms, the SwiGLU and the greedy argmax fused into them.
 
-    Per layer: q/k/v (one launch: they share their input), o, gate/up (one
-    launch), down; then the head: 32 x 4 + 1 = 129 launches per token."""
+    Per layer: RMSNorm + q/k/v (one launch: they share their input), o,
+    RMSNorm + gate/up + SwiGLU (one launch), down on h; then the final
+    RMSNorm + head + argmax: 32 x 4 + 1 = 129 launches per token."""
+    import numpy as np
     H, F, KV, V, L = 4096, 14336, 1024, 128256, 32
     print("[bench] building the 32-layer decode weight set", file=sys.stderr, flush=True)
     q4k_hh = synth.q4k_blocks(200, H, H)
@@ -378,16 +381,30 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     P = lambda t: t.data_ptr()
 
     h = torch.empty(F, device="cuda")
+    nw = torch.from_numpy(synth.normal(5, H, 0.1) + np.float32(1.0)).cuda()  # RMSNorm weight vectors
+    eps = 1e-5
 
-    def token(sp):
-        # per layer: q/k/v in one launch, o, gate/up + SwiGLU in one launch (h),
-        # down on h; then the head. Attention and norms are not part of this path.
+    def token(sp, norms=True):
+        # per layer: RMSNorm + q/k/v in one launch, o, RMSNorm + gate/up + SwiGLU
+        # in one launch (h), down on h; then the final RMSNorm + head + greedy
+        # argmax in one launch. Attention and the residual adds are not part
+        # of this path (they read q/k/v and write the next x). norms=False: the
+        # same launches without the fused RMSNorm prologues.
         for wq, wk, wv, wo, wg, wu, wd in layer_ws:
-            sq.matmul_multi_dev([wq, wk, wv], P(xh), 1, H, [P(q), P(k), P(v)], sp)
+            if norms:
+                sq.rmsnorm_matmul_multi_dev([wq, wk, wv], P(xh), P(nw), eps, 1, H, [P(q), P(k), P(v)], sp)
+            else:
+                sq.matmul_multi_dev([wq, wk, wv], P(xh), 1, H, [P(q), P(k), P(v)], sp)
             sq.matmul_dev(wo, P(xh), 1, H, P(o), sp)
-            sq.matmul_swiglu_dev(wg, wu, P(xh), 1, H, P(h), 0, 0, sp)
+            if norms:
+                sq.rmsnorm_matmul_swiglu_dev(wg, wu, P(xh), P(nw), eps, 1, H, P(h), sp)
+            else:
+                sq.matmul_swiglu_dev(wg, wu, P(xh), 1, H, P(h), 0, 0, sp)
             sq.matmul_dev(wd, P(h), 1, F, P(dn), sp)
-        sq.matmul_argmax_dev(head, P(xh), P(tok), 0, sp)  # head + greedy argmax, one launch
+        if norms:
+            sq.rmsnorm_matmul_argmax_dev(head, P(xh), P(nw), eps, P(tok), 0, sp)
+        else:
+            sq.matmul_argmax_dev(head, P(xh), P(tok), 0, sp)
 
     def timed(run) -> float:
         a = torch.cuda.Event(enable_timing=True)
@@ -403,8 +420,13 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
         token(stream.cuda_stream)
     torch.cuda.synchronize()
     ms = timed(lambda: token(stream.cuda_stream))
+    token(stream.cuda_stream, norms=False)
+    torch.cuda.synchronize()
+    ms_plain = timed(lambda: token(stream.cuda_stream, norms=False))
     # The same 129 launches captured once in a HIP graph and replayed: the
     # GEMV path allocates nothing and issues no memset, so it captures as is.
+    token(stream.cuda_stream)  # the captured token's own eager outputs are the reference
+    torch.cuda.synchronize()
     ref = (tok.clone(), dn.clone(), h.clone())
     cs = torch.cuda.Stream()
     with torch.cuda.stream(cs):
@@ -443,6 +465,7 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     del layer_ws, head
     torch.cuda.empty_cache()
     return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
+            "decode_gemv_tok_s_without_norms": round(1e3 / ms_plain, 1),
             "decode_gemv_tok_s_graph": round(1e3 / ms_graph, 1),
             "decode_gemv_ms_per_token_graph": round(ms_graph, 4),
             "decode_graph_replay_matches_eager": same,
@@ -450,9 +473,10 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
             "decode_gemv_GBps": round(tok_bytes / (ms * 1e-3) / 1e9, 1),
             "decode_gemv_GBps_graph": round(tok_bytes / (ms_graph * 1e-3) / 1e9, 1),
             "decode_host_entry_tok_s": round(1e3 / ms_host, 1),
-            "decode_note": "129 launches per token (32 layers x [qkv, o, gate/up+SwiGLU, down] + head with greedy "
-                           "argmax), device-resident, eager on one stream and replayed from one HIP graph; "
-                           "decode_host_entry_"
+            "decode_note": "129 launches per token (32 layers x [RMSNorm+qkv, o, RMSNorm+gate/up+SwiGLU, down] + "
+                           "final RMSNorm+head+greedy argmax), device-resident, eager on one stream and replayed "
+                           "from one HIP graph; _without_norms: the same launches without the RMSNorm "
+                           "prologues; decode_host_entry_"
                            "tok_s: the same 129 calls through the host-buffer entry points (x in, dst out, "
                            "synchronous, from Python); attention and norms not included"}
 

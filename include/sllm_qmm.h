@@ -162,6 +162,32 @@ sllm_status sllm_matmul_swiglu_dev(const sllm_weight *w_gate, const sllm_weight 
                                    int x_rows, int x_cols, float *h_dev, float *gate_dev, float *up_dev,
                                    void *stream);
 
+/*
+ * The RMSNorm in front of a layer's matmuls, fused into the GEMV prologue:
+ * rmsNormFlatF32 (float32_ops.go:159-172) of each activation row with weight
+ * vector norm_w_dev (x_cols floats) and eps, then the matmuls of
+ * sllm_matmul_multi_dev / sllm_matmul_swiglu_dev / sllm_matmul_argmax_dev on
+ * the normed rows (forwardBlock: model_f32.go:388-396 and 476-490;
+ * outputLogits: model_f32.go:502-527). For one row (decode) the GEMV launch
+ * computes the row statistic itself, so no normed vector goes through memory;
+ * several rows are normed into the workspace first by a standalone kernel
+ * with the same statistics. inv = 1 / float32(sqrt(
+ * float64(ss) / cols + float64(eps))) and normed = (x * inv) * w as in the
+ * reference; the sum of squares ss is added in a fixed order of the library's
+ * (256 strided partial sums, then a fixed tree) rather than the reference's
+ * single sequential loop, so only its association differs. x_dev and
+ * norm_w_dev must be 16-byte aligned.
+ */
+sllm_status sllm_rmsnorm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x_dev,
+                                          const float *norm_w_dev, float eps, int x_rows, int x_cols,
+                                          float *const *dst_dev, void *stream);
+sllm_status sllm_rmsnorm_matmul_swiglu_dev(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x_dev,
+                                           const float *norm_w_dev, float eps, int x_rows, int x_cols,
+                                           float *h_dev, void *stream);
+sllm_status sllm_rmsnorm_matmul_argmax_dev(const sllm_weight *w, const float *x_dev, const float *norm_w_dev,
+                                           float eps, int x_cols, float *logits_dev, int *argmax_dev,
+                                           void *stream);
+
 /* Host-buffer form of sllm_matmul_swiglu_dev (synchronous; h only). */
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,
                                         int x_rows, int x_cols, float *h);

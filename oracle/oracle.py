@@ -79,6 +79,8 @@ def lib() -> C.CDLL:
         L.ref_swiglu.restype = C.c_float
         L.ref_swiglu.argtypes = [C.c_float, C.c_float]
         L.ref_swiglu_n.argtypes = [P, P, P, i64]
+        L.ref_rmsnorm.argtypes = [P, P, C.c_float, i32, i32, P]
+        L.ref_rmsnorm_lib.argtypes = [P, P, C.c_float, i32, i32, P]
         _lib = L
     return _lib
 
@@ -207,6 +209,19 @@ def swiglu(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     h = np.empty_like(g)
     lib().ref_swiglu_n(_p(g), _p(u), _p(h), g.size)
     return h.reshape(np.shape(gate))
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, lib_order: bool = False) -> np.ndarray:
+    """rmsNormFlatF32 (float32_ops.go:159-172) of every row of x; lib_order: the
+    library's association of the sum of squares instead of the reference's."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    K = x.shape[-1]
+    rows = x.size // K
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.empty_like(x)
+    fn = lib().ref_rmsnorm_lib if lib_order else lib().ref_rmsnorm
+    fn(_p(x), _p(w), eps, rows, K, _p(out))
+    return out
 
 
 def argmax(v: np.ndarray) -> int:

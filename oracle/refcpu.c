@@ -751,3 +751,64 @@ float ref_swiglu(float gate, float up) {
 void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n) {
     for (int64_t i = 0; i < n; i++) h[i] = ref_swiglu(gate[i], up[i]);
 }
+
+/* rmsNormFlatF32 (float32_ops.go:159-172), per row:
+ *   ss += v*v (float32, sequential); inv := 1.0 / float32(math.Sqrt(float64(ss)/float64(cols)+float64(eps)))
+ *   out[j] = x[j] * inv * w[j]  (float32, left to right) */
+static void rms_apply(const float *x, const float *w, float ss, float eps, int cols, float *out) {
+    float inv = 1.0f / (float)sqrt((double)ss / (double)cols + (double)eps);
+    for (int j = 0; j < cols; j++) {
+        float t = x[j] * inv;
+        out[j] = t * w[j];
+    }
+}
+
+void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * cols;
+        float ss = 0.0f;
+        for (int j = 0; j < cols; j++) {
+            float sq = xr[j] * xr[j];
+            ss = ss + sq;
+        }
+        rms_apply(xr, w, ss, eps, cols, out + (size_t)r * cols);
+    }
+}
+
+/* The same norm with the sum of squares in the library's association (its
+ * fused GEMV prologue and prefill pre-pass): 256 slot sums, slot s adding
+ * x[s]^2, x[s+256]^2, ... in order; each group of 64 slots added as a wave
+ * reduction does it (pairs, quads, groups of 8 and of 16 as balanced trees,
+ * then the four 16-slot sums left to right); the four 64-slot sums left to
+ * right. Test infrastructure: it lets the GPU path be checked bit for bit;
+ * ref_rmsnorm above is the reference's order. */
+static float tree16(const float *v) {
+    float a[16];
+    for (int i = 0; i < 16; i++) a[i] = v[i];
+    for (int w = 1; w < 16; w *= 2)
+        for (int i = 0; i < 16; i += 2 * w) a[i] = a[i] + a[i + w];
+    return a[0];
+}
+
+void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out) {
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (size_t)r * cols;
+        float slot[256];
+        for (int s = 0; s < 256; s++) {
+            float p = 0.0f;
+            for (int i = s; i < cols; i += 256) {
+                float sq = xr[i] * xr[i];
+                p = p + sq;
+            }
+            slot[s] = p;
+        }
+        float waves[4];
+        for (int q = 0; q < 4; q++) {
+            float r16[4];
+            for (int k = 0; k < 4; k++) r16[k] = tree16(slot + 64 * q + 16 * k);
+            waves[q] = ((r16[0] + r16[1]) + r16[2]) + r16[3];
+        }
+        float ss = ((waves[0] + waves[1]) + waves[2]) + waves[3];
+        rms_apply(xr, w, ss, eps, cols, out + (size_t)r * cols);
+    }
+}

@@ -24,6 +24,11 @@ extern "C" {
 float ref_swiglu(float gate, float up);
 void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
 
+/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
+ * the library's sum-of-squares association. */
+void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
+void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
+
 #endif
 
 /* ---- f16 codecs -------------------------------------------------------- */
@@ -108,9 +113,19 @@ int ref_block_bytes(const char *qtype);
 float ref_swiglu(float gate, float up);
 void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
 
+/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
+ * the library's sum-of-squares association. */
+void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
+void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
+
 #endif
 /* model_f32.go:486-489 SwiGLU, one element and n elements. */
 float ref_swiglu(float gate, float up);
 void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
+
+/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
+ * the library's sum-of-squares association. */
+void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
+void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
 
 #endif

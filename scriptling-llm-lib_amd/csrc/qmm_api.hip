@@ -67,7 +67,9 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
             p = nullptr;
             return set_error(SLLM_ERR_OOM, "argmax scratch allocation failed");
         }
-        SLLM_HIP(hipMemset(p, 0, 64));
+        // cleared on the stream that uses it: a non-blocking stream is not
+        // ordered after the null stream, where hipMemset would run
+        SLLM_HIP(hipMemsetAsync(p, 0, 64, stream));
     }
     *out = p;
     return SLLM_OK;
@@ -231,6 +233,107 @@ sllm_status run_matmul(const sllm_weight *w, const float *x, int x_rows, float *
     const Planes P = as_const(w->planes);
     if (!uses_gemm(w, x_rows)) return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
     return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
+}
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// GEMM activation workspace the GEMM-bound weights of a set need (the largest).
+size_t multi_gemm_ws(const sllm_weight *const *ws, int count, int x_rows) {
+    size_t need = 0;
+    for (int i = 0; i < count; i++)
+        if (uses_gemm(ws[i], x_rows)) {
+            const size_t b = gemm_workspace_bytes(ws[i]->fmt, ws[i]->rows, ws[i]->groups, x_rows);
+            need = b > need ? b : need;
+        }
+    return align256(need);
+}
+
+// Weights sharing the activation rows x. GEMV weights are grouped by format,
+// up to kMaxSegs per launch (with the RMSNorm prologue when nw is given);
+// GEMM-bound weights run one by one with the workspace [gws, gws + gcap).
+sllm_status multi_impl(const sllm_weight *const *ws, int count, const float *x, int x_rows, float *const *dst,
+                       hipStream_t s, void *gws, size_t gcap, const float *nw, float eps) {
+    sllm_status st = SLLM_OK;
+    std::vector<char> done((size_t)count, 0);
+    for (int i = 0; i < count; i++) {
+        if (done[(size_t)i]) continue;
+        const sllm_weight *w = ws[i];
+        if (uses_gemm(w, x_rows)) {
+            done[(size_t)i] = 1;
+            if ((st = run_matmul(w, x, x_rows, dst[i], s, gws, gcap)) != SLLM_OK) return st;
+            continue;
+        }
+        Planes P[kMaxSegs];
+        float *D[kMaxSegs];
+        int N[kMaxSegs];
+        int n = 0;
+        for (int j = i; j < count && n < kMaxSegs; j++) {
+            if (done[(size_t)j] || ws[j]->fmt != w->fmt || uses_gemm(ws[j], x_rows)) continue;
+            P[n] = as_const(ws[j]->planes);
+            D[n] = dst[j];
+            N[n] = ws[j]->rows;
+            n++;
+            done[(size_t)j] = 1;
+        }
+        if ((st = launch_gemv_multi(w->fmt, P, D, N, n, x, w->groups, x_rows, s, nw, eps)) != SLLM_OK) return st;
+    }
+    return SLLM_OK;
+}
+
+// Whether gate / up fit the one paired GEMV launch.
+bool swiglu_paired(const sllm_weight *wg, const sllm_weight *wu, int x_rows) {
+    return !uses_gemm(wg, x_rows) && !uses_gemm(wu, x_rows) && wg->fmt == wu->fmt;
+}
+
+// Workspace the unpaired SwiGLU path needs: the GEMM workspace, then gate / up
+// buffers the caller did not provide.
+size_t swiglu_ws_bytes(const sllm_weight *wg, const sllm_weight *wu, int x_rows, const float *gate,
+                       const float *up) {
+    if (swiglu_paired(wg, wu, x_rows)) return 0;
+    const sllm_weight *pair[2] = {wg, wu};
+    const size_t mm = align256((size_t)x_rows * wg->rows * sizeof(float));
+    return multi_gemm_ws(pair, 2, x_rows) + (gate ? 0 : mm) + (up ? 0 : mm);
+}
+
+sllm_status swiglu_impl(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows, float *h,
+                        float *gate, float *up, hipStream_t s, void *ws, const float *nw, float eps) {
+    const int N = wg->rows;
+    if (swiglu_paired(wg, wu, x_rows))
+        return launch_gemv_swiglu(wg->fmt, as_const(wg->planes), as_const(wu->planes), x, h, gate, up, N,
+                                  wg->groups, x_rows, s, nw, eps);
+    // Prefill or mixed formats: the two matmuls, then the elementwise SwiGLU;
+    // x is already normed here (nw is only passed for the paired launch).
+    const sllm_weight *pair[2] = {wg, wu};
+    const size_t gw = multi_gemm_ws(pair, 2, x_rows);
+    const size_t mm = align256((size_t)x_rows * N * sizeof(float));
+    char *tail = (char *)ws + gw;
+    float *g = gate ? gate : (float *)tail;
+    float *u = up ? up : (float *)(tail + (gate ? 0 : mm));
+    sllm_status st;
+    if ((st = run_matmul(wg, x, x_rows, g, s, ws, gw)) != SLLM_OK) return st;
+    if ((st = run_matmul(wu, x, x_rows, u, s, ws, gw)) != SLLM_OK) return st;
+    return launch_swiglu(g, u, h, (size_t)x_rows * N, s);
+}
+
+sllm_status check_multi(const sllm_weight *const *ws, int count, const float *x, int x_rows, int x_cols,
+                        float *const *dst) {
+    if (!ws || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (count <= 0) return set_error(SLLM_ERR_ARG, "count must be positive");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    for (int i = 0; i < count; i++) {
+        if (!ws[i] || !dst[i]) return set_error(SLLM_ERR_ARG, "null weight or dst");
+        if (ws[i]->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match a weight's Cols");
+    }
+    return SLLM_OK;
+}
+
+sllm_status check_swiglu(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows, int x_cols,
+                         const float *h) {
+    if (!wg || !wu || !x || !h) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (wg->cols != x_cols || wu->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match Cols");
+    if (wg->rows != wu->rows) return set_error(SLLM_ERR_ARG, "gate and up have different Rows");
+    return SLLM_OK;
 }
 
 bool check_shape(int rows, int cols, sllm_status *st) {
@@ -509,38 +612,39 @@ sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *t
 
 sllm_status sllm_matmul_swiglu_dev(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows,
                                    int x_cols, float *h, float *gate, float *up, void *stream) {
-    if (!wg || !wu || !x || !h) return set_error(SLLM_ERR_ARG, "null pointer");
-    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
-    if (wg->cols != x_cols || wu->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match Cols");
-    if (wg->rows != wu->rows) return set_error(SLLM_ERR_ARG, "gate and up have different Rows");
-    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
-    sllm_status st = ensure_init();
+    sllm_status st = check_swiglu(wg, wu, x, x_rows, x_cols, h);
     if (st != SLLM_OK) return st;
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    if ((st = ensure_init()) != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    const int N = wg->rows;
-    if (!uses_gemm(wg, x_rows) && !uses_gemm(wu, x_rows) && wg->fmt == wu->fmt)
-        return launch_gemv_swiglu(wg->fmt, as_const(wg->planes), as_const(wu->planes), x, h, gate, up, N,
-                                  wg->groups, x_rows, s);
-    // Prefill or mixed formats: the two matmuls, then the elementwise SwiGLU.
-    // gate / up land in the caller's buffers or after the GEMM workspace.
-    const size_t mm = (size_t)x_rows * N * sizeof(float);
-    size_t gw = 0;
-    if (uses_gemm(wg, x_rows)) gw = gemm_workspace_bytes(wg->fmt, N, wg->groups, x_rows);
-    if (uses_gemm(wu, x_rows)) {
-        const size_t g2 = gemm_workspace_bytes(wu->fmt, N, wu->groups, x_rows);
-        gw = g2 > gw ? g2 : gw;
-    }
-    gw = (gw + 255) & ~(size_t)255;
-    const size_t extra = (gate ? 0 : ((mm + 255) & ~(size_t)255)) + (up ? 0 : mm);
     void *ws = nullptr;
     size_t cap = 0;
-    if (gw + extra > 0 && (st = workspace(s, gw + extra, &ws, &cap)) != SLLM_OK) return st;
-    char *tail = (char *)ws + gw;
-    float *g = gate ? gate : (float *)tail;
-    float *u = up ? up : (float *)(tail + (gate ? 0 : ((mm + 255) & ~(size_t)255)));
-    if ((st = run_matmul(wg, x, x_rows, g, s, ws, gw)) != SLLM_OK) return st;
-    if ((st = run_matmul(wu, x, x_rows, u, s, ws, gw)) != SLLM_OK) return st;
-    return launch_swiglu(g, u, h, (size_t)x_rows * N, s);
+    const size_t need = swiglu_ws_bytes(wg, wu, x_rows, gate, up);
+    if (need && (st = workspace(s, need, &ws, &cap)) != SLLM_OK) return st;
+    return swiglu_impl(wg, wu, x, x_rows, h, gate, up, s, ws, nullptr, 0.0f);
+}
+
+sllm_status sllm_rmsnorm_matmul_swiglu_dev(const sllm_weight *wg, const sllm_weight *wu, const float *x,
+                                           const float *norm_w, float eps, int x_rows, int x_cols, float *h,
+                                           void *stream) {
+    sllm_status st = check_swiglu(wg, wu, x, x_rows, x_cols, h);
+    if (st != SLLM_OK) return st;
+    if (!norm_w) return set_error(SLLM_ERR_ARG, "null norm weight");
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)norm_w & 15) != 0)
+        return set_error(SLLM_ERR_ARG, "x and the norm weight must be 16-byte aligned");
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    // one row (decode) with a paired gate / up: the norm is the GEMV's prologue
+    if (x_rows == 1 && swiglu_paired(wg, wu, x_rows))
+        return swiglu_impl(wg, wu, x, x_rows, h, nullptr, nullptr, s, nullptr, norm_w, eps);
+    // several rows / mixed formats: normed rows into the workspace first
+    const size_t nb = align256((size_t)x_rows * x_cols * sizeof(float));
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, nb + swiglu_ws_bytes(wg, wu, x_rows, nullptr, nullptr), &ws, &cap)) != SLLM_OK) return st;
+    float *normed = (float *)ws;
+    if ((st = launch_rmsnorm(x, norm_w, eps, x_rows, x_cols, normed, s)) != SLLM_OK) return st;
+    return swiglu_impl(wg, wu, normed, x_rows, h, nullptr, nullptr, s, (char *)ws + nb, nullptr, 0.0f);
 }
 
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *wg, const sllm_weight *wu, const float *x, int x_rows,
@@ -599,42 +703,55 @@ sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int
 
 sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x, int x_rows, int x_cols,
                                   float *const *dst, void *stream) {
-    if (!ws || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
-    if (count <= 0) return set_error(SLLM_ERR_ARG, "count must be positive");
-    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
-    for (int i = 0; i < count; i++) {
-        if (!ws[i] || !dst[i]) return set_error(SLLM_ERR_ARG, "null weight or dst");
-        if (ws[i]->cols != x_cols) return set_error(SLLM_ERR_ARG, "xCols does not match a weight's Cols");
-    }
+    sllm_status st = check_multi(ws, count, x, x_rows, x_cols, dst);
+    if (st != SLLM_OK) return st;
     if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    void *gws = nullptr;
+    size_t cap = 0;
+    const size_t need = multi_gemm_ws(ws, count, x_rows);
+    if (need && (st = workspace(s, need, &gws, &cap)) != SLLM_OK) return st;
+    return multi_impl(ws, count, x, x_rows, dst, s, gws, need, nullptr, 0.0f);
+}
+
+sllm_status sllm_rmsnorm_matmul_multi_dev(const sllm_weight *const *ws, int count, const float *x,
+                                          const float *norm_w, float eps, int x_rows, int x_cols,
+                                          float *const *dst, void *stream) {
+    sllm_status st = check_multi(ws, count, x, x_rows, x_cols, dst);
+    if (st != SLLM_OK) return st;
+    if (!norm_w) return set_error(SLLM_ERR_ARG, "null norm weight");
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)norm_w & 15) != 0)
+        return set_error(SLLM_ERR_ARG, "x and the norm weight must be 16-byte aligned");
+    if ((st = ensure_init()) != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const size_t gneed = multi_gemm_ws(ws, count, x_rows);
+    // one row (decode): the norm is the GEMV's prologue
+    if (x_rows == 1 && gneed == 0) return multi_impl(ws, count, x, x_rows, dst, s, nullptr, 0, norm_w, eps);
+    // several rows: normed rows into the workspace first, then every weight
+    // reads them (GEMV and GEMM alike)
+    const size_t nb = align256((size_t)x_rows * x_cols * sizeof(float));
+    void *ws_ = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, nb + gneed, &ws_, &cap)) != SLLM_OK) return st;
+    float *normed = (float *)ws_;
+    if ((st = launch_rmsnorm(x, norm_w, eps, x_rows, x_cols, normed, s)) != SLLM_OK) return st;
+    return multi_impl(ws, count, normed, x_rows, dst, s, (char *)ws_ + nb, gneed, nullptr, 0.0f);
+}
+
+sllm_status sllm_rmsnorm_matmul_argmax_dev(const sllm_weight *w, const float *x, const float *norm_w, float eps,
+                                           int x_cols, float *logits, int *argmax, void *stream) {
+    if (!w || !x || !norm_w || !argmax) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_cols != w->cols) return set_error(SLLM_ERR_ARG, "xCols does not match the weight's Cols");
+    if (((uintptr_t)x & 15) != 0 || ((uintptr_t)norm_w & 15) != 0)
+        return set_error(SLLM_ERR_ARG, "x and the norm weight must be 16-byte aligned");
     sllm_status st = ensure_init();
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    // weights that take the GEMV: grouped by format, up to kMaxSegs per launch
-    std::vector<char> done((size_t)count, 0);
-    for (int i = 0; i < count; i++) {
-        if (done[(size_t)i]) continue;
-        const sllm_weight *w = ws[i];
-        if (uses_gemm(w, x_rows)) {
-            done[(size_t)i] = 1;
-            if ((st = sllm_matmul_dev(w, x, x_rows, x_cols, dst[i], stream)) != SLLM_OK) return st;
-            continue;
-        }
-        Planes P[kMaxSegs];
-        float *D[kMaxSegs];
-        int N[kMaxSegs];
-        int n = 0;
-        for (int j = i; j < count && n < kMaxSegs; j++) {
-            if (done[(size_t)j] || ws[j]->fmt != w->fmt) continue;
-            P[n] = as_const(ws[j]->planes);
-            D[n] = dst[j];
-            N[n] = ws[j]->rows;
-            n++;
-            done[(size_t)j] = 1;
-        }
-        if ((st = launch_gemv_multi(w->fmt, P, D, N, n, x, w->groups, x_rows, s)) != SLLM_OK) return st;
-    }
-    return SLLM_OK;
+    void *scr = nullptr;
+    if ((st = amax_scratch(s, &scr)) != SLLM_OK) return st;
+    return launch_gemv_argmax(w->fmt, as_const(w->planes), x, logits, w->rows, w->groups,
+                              (unsigned long long *)scr, (unsigned int *)((char *)scr + 8), argmax, s, norm_w, eps);
 }
 
 sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int count, const float *x, int x_rows,

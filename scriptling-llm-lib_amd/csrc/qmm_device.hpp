@@ -45,16 +45,6 @@ __device__ __forceinline__ uint16_t f64_to_f16_trunc(double f) {
 
 // ------------------------------------------------- activation quantizer ----
 
-// Go's int32(float32) on amd64 (CVTTSS2SL) followed by the clamp of
-// quantizeActivationsQ8: truncation toward zero; NaN, +-Inf and values outside
-// int32 become INT32_MIN and so clamp to -128.
-__device__ __forceinline__ int quant_trunc_clamp(float p) {
-    int q = (p >= -2147483648.0f && p < 2147483648.0f) ? (int)p : INT32_MIN;
-    q = q > 127 ? 127 : q;
-    q = q < -128 ? -128 : q;
-    return q;
-}
-
 // Combine a value across the TPB consecutive, aligned lanes that share a block
 // (TPB = 1, 2, 4 or 8) with DPP moves; every lane of the group receives it.
 template <int CTRL>
@@ -85,9 +75,11 @@ __device__ __forceinline__ int group_sum(int v) {
 // 1/scale in IEEE fp32 (0 for an all-zero block), q = clamp(int32(x*inv)).
 // The maximum and the integer sum do not depend on how the lanes combine.
 //
-// Per element this is quant_trunc_clamp(x * inv) in fewer operations: the
-// product is clamped in float first (fmaxf returns -128 for a NaN product,
-// and trunc(clamp(t)) == clamp(trunc(t)) for every finite or infinite t), then
+// Per element the reference computes Go's int32(float32) on amd64
+// (CVTTSS2SL: truncation toward zero; NaN, +-Inf and values outside int32
+// become INT32_MIN) and clamps that to [-128, 127]. Here the product is
+// clamped in float first (fmaxf returns -128 for a NaN product, and
+// trunc(clamp(t)) == clamp(trunc(t)) for every finite or infinite t), then
 // truncated. The one case where the two differ is a +Inf product, which Go
 // sends to INT32_MIN and so to -128: x * inv is +Inf only when inv itself is
 // +Inf (the block's scale underflowed to 0 or below 1/FLT_MAX), and then every

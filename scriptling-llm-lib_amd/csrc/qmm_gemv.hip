@@ -57,8 +57,9 @@ namespace {
 // pair: P[0] / P[1] are the gate / up weights of one FFN (N[0] == N[1]) and
 // dst[0..2] receive SwiGLU(gate, up), gate (may be null), up (may be null).
 sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const int *N, int nseg, bool pair,
-                            const float *x, int G, int M, hipStream_t s, unsigned long long *amax_key = nullptr,
-                            unsigned int *amax_cnt = nullptr, int *amax_out = nullptr) {
+                            const float *x, int G, int M, hipStream_t s, const float *norm_w, float eps,
+                            unsigned long long *amax_key = nullptr, unsigned int *amax_cnt = nullptr,
+                            int *amax_out = nullptr) {
     if (nseg < 1 || nseg > kMaxSegs) return set_error(SLLM_ERR_ARG, "gemv: 1 to 4 weights per launch");
     if (G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
     if (pair && (nseg != 2 || N[0] != N[1])) return set_error(SLLM_ERR_ARG, "gemv: gate / up shapes differ");
@@ -109,11 +110,14 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
     const int grid = (int)((waves + W - 1) / W);
     if (amax_key && (M != 1 || nseg != 1 || pair)) return set_error(SLLM_ERR_ARG, "gemv: argmax needs one row");
+    if (norm_w && M != 1) return set_error(SLLM_ERR_ARG, "gemv: the fused RMSNorm takes one activation row");
     SegTable S{};
     S.n = nrow_segs;
     S.amax_key = amax_key;
     S.amax_cnt = amax_cnt;
     S.amax_out = amax_out;
+    S.norm_w = norm_w;
+    S.norm_eps = eps;
     S.wave0[0] = 0;
     for (int i = 0; i < nseg; i++) {
         S.P[i] = P[i];
@@ -167,16 +171,17 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
 }  // namespace
 
 sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
-                              const float *x, int G, int M, hipStream_t s) {
-    return plan_and_launch(fmt, P, dst, N, nseg, false, x, G, M, s);
+                              const float *x, int G, int M, hipStream_t s, const float *norm_w, float eps) {
+    return plan_and_launch(fmt, P, dst, N, nseg, false, x, G, M, s, norm_w, eps);
 }
 
 sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, const float *x, float *h,
-                               float *gate, float *up, int N, int G, int M, hipStream_t s) {
+                               float *gate, float *up, int N, int G, int M, hipStream_t s, const float *norm_w,
+                               float eps) {
     const Planes P[2] = {Pg, Pu};
     float *const dst[3] = {h, gate, up};
     const int Ns[2] = {N, N};
-    return plan_and_launch(fmt, P, dst, Ns, 2, true, x, G, M, s);
+    return plan_and_launch(fmt, P, dst, Ns, 2, true, x, G, M, s, norm_w, eps);
 }
 
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
@@ -185,8 +190,28 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
 }
 
 sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
-                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s) {
-    return plan_and_launch(fmt, &P, &logits, &N, 1, false, x, G, 1, s, key, cnt, out);
+                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s,
+                               const float *norm_w, float eps) {
+    return plan_and_launch(fmt, &P, &logits, &N, 1, false, x, G, 1, s, norm_w, eps, key, cnt, out);
+}
+
+namespace {
+// One workgroup of 256 threads per row: the same statistics as the GEMV
+// prologue (rms_inv), then normed = (x * inv) * w.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float *__restrict__ x, const float *__restrict__ nw,
+                                                      float eps, int K, float *__restrict__ out) {
+    __shared__ float red[4];
+    const size_t off = (size_t)blockIdx.x * K;
+    const float inv = rms_inv<16>(x + off, K, eps, red);
+    for (int i = threadIdx.x; i < K; i += 256) out[off + i] = (x[off + i] * inv) * nw[i];
+}
+}  // namespace
+
+sllm_status launch_rmsnorm(const float *x, const float *norm_w, float eps, int rows, int K, float *out,
+                           hipStream_t s) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(256), 0, s, x, norm_w, eps, K, out);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
 }
 
 // ------------------------------------------------------ verification ----

@@ -241,6 +241,103 @@ __device__ __forceinline__ void prologue(BlockRegs (&buf)[D][NB], const float *_
     }
 }
 
+// rmsNormFlatF32 (float32_ops.go:159-172) statistics of one K-element row,
+// called by every thread of a workgroup of >= 256 threads: the sum of squares
+// over a fixed partition - slot s (s < 256) adds v*v for v = xr[s], xr[s+256],
+// ... in that order, then the 256 slot sums are added by wave_sum within each
+// of the first four waves and the four results left to right - so every launch
+// shape gives the same value. Then inv = 1 / float32(sqrt(float64(ss) /
+// float64(K) + float64(eps))), as the reference computes it. The reference
+// adds the squares in one sequential loop; only that association differs.
+//
+// Split in two so that a caller can issue other loads between them: rms_load
+// issues slot t's next RB loads (past the row's end they read as 0, and adding
+// 0*0 leaves a non-negative sum unchanged), rms_finish adds them and the rest.
+template <int RB>
+__device__ __forceinline__ void rms_load(const float *__restrict__ xr, int K, int i, float (&v)[RB]) {
+#pragma unroll
+    for (int k = 0; k < RB; k++) v[k] = i + k * 256 < K ? xr[i + k * 256] : 0.0f;
+}
+template <int RB>
+__device__ __forceinline__ float rms_finish(const float *__restrict__ xr, int K, float eps, float *red,
+                                            float (&v)[RB]) {
+    const int t = threadIdx.x;
+    float p = 0.0f;
+    if (t < 256) {
+        for (int i = t;;) {
+#pragma unroll
+            for (int k = 0; k < RB; k++) p = p + v[k] * v[k];
+            i += RB * 256;
+            if (i >= K) break;
+            rms_load<RB>(xr, K, i, v);
+        }
+    }
+    const float w = wave_sum(p);
+    if (t < 256 && (t & 63) == 0) red[t >> 6] = w;
+    __syncthreads();
+    const float ss = ((red[0] + red[1]) + red[2]) + red[3];
+    const double ms = (double)ss / (double)K + (double)eps;
+    const float inv = 1.0f / (float)sqrt(ms);
+    __syncthreads();  // red may be reused
+    return inv;
+}
+template <int RB = 16>
+__device__ __forceinline__ float rms_inv(const float *__restrict__ xr, int K, float eps, float *red) {
+    float v[RB];
+    if (threadIdx.x < 256) rms_load<RB>(xr, K, threadIdx.x, v);
+    return rms_finish<RB>(xr, K, eps, red, v);
+}
+
+// The prologue with the RMSNorm in front of the quantizer, for one activation
+// row: the row's statistics loads go out first, then this thread's first
+// block of x and of the norm weight, then the wave's first D weight units;
+// the statistics are then reduced and each block of (x * inv) * w quantized
+// into LDS. (Loads return in order: anything issued after the weight units
+// would wait for them.)
+template <int FMT, int NB, int D, int TPB, class Issue>
+__device__ __forceinline__ void prologue_norm(BlockRegs (&buf)[D][NB], const float *__restrict__ x,
+                                              const float *__restrict__ nw, float eps, int G, const ActView &A,
+                                              Issue &issue) {
+    __shared__ float red[4];
+    constexpr int NV = 8 / TPB;
+    // fewer statistics loads in flight where the weight ring holds many registers
+    constexpr int RB = NB * D >= 6 ? 4 : 16;
+    // the first block's operands are preloaded where they are few registers
+    // and the ring leaves room for them
+    constexpr bool PRE = NV <= 2 && NB * D < 6;
+    const int K = G * 32;
+    float v[RB];
+    if (threadIdx.x < 256) rms_load<RB>(x, K, threadIdx.x, v);
+    const int sub = threadIdx.x % TPB;
+    const int blk0 = threadIdx.x / TPB;
+    float4 xa[PRE ? NV : 1], wa[PRE ? NV : 1];
+    if (PRE) {
+        const int bc = blk0 < G ? blk0 : 0;
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            xa[PRE ? k : 0] = ((const float4 *)(x + (size_t)bc * 32) + sub * NV)[k];
+            wa[PRE ? k : 0] = ((const float4 *)(nw + (size_t)bc * 32) + sub * NV)[k];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < D; d++) issue(buf[d]);
+    __builtin_amdgcn_sched_barrier(0);
+    const float inv = rms_finish<RB>(x, K, eps, red, v);
+    const int per_pass = blockDim.x / TPB;
+    for (int b = blk0; b < G; b += per_pass) {
+        float4 q[NV];
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            const float4 a = PRE && b == blk0 ? xa[PRE ? k : 0] : ((const float4 *)(x + (size_t)b * 32) + sub * NV)[k];
+            const float4 c = PRE && b == blk0 ? wa[PRE ? k : 0] : ((const float4 *)(nw + (size_t)b * 32) + sub * NV)[k];
+            // float32_ops.go:169: out = x * inv * w, left to right
+            q[k] = make_float4((a.x * inv) * c.x, (a.y * inv) * c.y, (a.z * inv) * c.z, (a.w * inv) * c.w);
+        }
+        stage_part<FMT, TPB>(q, b, sub, A);
+    }
+}
+
 // The weights of one launch (same format, same K, same activation rows).
 // Segment s owns the waves [wave0[s], wave0[s + 1]) of the grid; wave0[n] is
 // the grid's wave count, so the last segment also takes the spare waves.
@@ -256,6 +353,8 @@ struct SegTable {
     int N[kMaxSegs];
     int wave0[kMaxSegs + 1];
     int n;
+    const float *norm_w;  // non-null: RMSNorm the activation rows first (weight vector, eps)
+    float norm_eps;
     unsigned long long *amax_key;
     unsigned int *amax_cnt;  // [0] workgroups done, [1] row 0 is NaN
     int *amax_out;
@@ -293,14 +392,18 @@ __device__ __forceinline__ void argmax_tail(const SegTable &S, float v, bool min
         if (best) atomicMax(S.amax_key, best);
         __threadfence();
         if (atomicAdd(&S.amax_cnt[0], 1u) == gridDim.x - 1) {
+            // every other workgroup's max landed before its count (fence, then
+            // count). Key and flag are read with device-scope atomic loads
+            // issued together, and cleared with device-scope atomic stores
+            // (the next launch on this stream starts after this one completes)
             __threadfence();
-            const unsigned long long fin = atomicAdd(S.amax_key, 0ull);
-            const unsigned int nan0 = atomicAdd(&S.amax_cnt[1], 0u);
+            const unsigned long long fin =
+                __hip_atomic_load(S.amax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned int nan0 = __hip_atomic_load(&S.amax_cnt[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *S.amax_out = (nan0 || fin == 0) ? 0 : (int)~(uint32_t)fin;
-            atomicExch(S.amax_key, 0ull);
-            atomicExch(&S.amax_cnt[1], 0u);
-            __threadfence();
-            atomicExch(&S.amax_cnt[0], 0u);
+            __hip_atomic_store(S.amax_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&S.amax_cnt[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&S.amax_cnt[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
@@ -311,7 +414,8 @@ __device__ __forceinline__ void argmax_tail(const SegTable &S, float v, bool min
 // flight in a register ring: it computes unit t, then issues the loads of
 // unit t + D into the registers it just consumed. PAIR: each row is streamed
 // twice, gate chunks then up chunks, and the wave combines the two sums.
-template <int FMT, int NB, int D, int MT, bool HOIST, bool PAIR>
+// NORM: the activation row (M == 1) is RMSNormed (S.norm_w, S.norm_eps) on the way in.
+template <int FMT, int NB, int D, int MT, bool HOIST, bool PAIR, bool NORM>
 __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__restrict__ x, int G, int M,
                                                     int KCH, int RPW, int tpb) {
     extern __shared__ __attribute__((aligned(16))) unsigned char lds[];
@@ -377,11 +481,18 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     // threads, TPB lanes per block. Each thread issues its activation loads,
     // then its wave's first D units of weights, then quantizes: it waits only
     // for its activation loads while the weight stream is in flight.
-    switch (tpb) {
-    case 8: prologue<FMT, NB, D, 8>(buf, x, M, G, A, issue); break;
-    case 4: prologue<FMT, NB, D, 4>(buf, x, M, G, A, issue); break;
-    case 2: prologue<FMT, NB, D, 2>(buf, x, M, G, A, issue); break;
-    default: prologue<FMT, NB, D, 1>(buf, x, M, G, A, issue); break;
+    if constexpr (NORM) {
+        // 8 or 4 lanes per block (the launch passes tpb >= 4): fewer would hold
+        // x, w and the normed values of a whole block per lane beside the ring
+        if (tpb == 8) prologue_norm<FMT, NB, D, 8>(buf, x, S.norm_w, S.norm_eps, G, A, issue);
+        else prologue_norm<FMT, NB, D, 4>(buf, x, S.norm_w, S.norm_eps, G, A, issue);
+    } else {
+        switch (tpb) {
+        case 8: prologue<FMT, NB, D, 8>(buf, x, M, G, A, issue); break;
+        case 4: prologue<FMT, NB, D, 4>(buf, x, M, G, A, issue); break;
+        case 2: prologue<FMT, NB, D, 2>(buf, x, M, G, A, issue); break;
+        default: prologue<FMT, NB, D, 1>(buf, x, M, G, A, issue); break;
+        }
     }
     __syncthreads();
 
@@ -500,13 +611,27 @@ sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, i
     constexpr bool kCanHoist = FMT != SLLM_Q5_0 && NB * MT <= 4;
     // lanes per activation block in the prologue: as many as the workgroup allows
     int tpb = 8;
-    while (tpb > 1 && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
-    if (kCanHoist && KCH == 1)
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist, PAIR>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M,
-                           KCH, RPW, tpb);
-    else
-        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false, PAIR>), dim3(grid), dim3(W * 64), lds, s, S, x, G, M, KCH,
-                           RPW, tpb);
+    while (tpb > (S.norm_w ? 4 : 1) && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
+    const bool hoist = kCanHoist && KCH == 1;
+    if (S.norm_w) {
+        // the fused RMSNorm prologue exists for one-row tiles (decode)
+        if constexpr (MT == 1) {
+            if (hoist)
+                hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist, PAIR, true>), dim3(grid), dim3(W * 64), lds,
+                                   s, S, x, G, M, KCH, RPW, tpb);
+            else
+                hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false, PAIR, true>), dim3(grid), dim3(W * 64), lds, s,
+                                   S, x, G, M, KCH, RPW, tpb);
+        } else {
+            return set_error(SLLM_ERR_SHAPE, "gemv: the fused RMSNorm takes one activation row");
+        }
+    } else if (hoist) {
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, kCanHoist, PAIR, false>), dim3(grid), dim3(W * 64), lds, s, S,
+                           x, G, M, KCH, RPW, tpb);
+    } else {
+        hipLaunchKernelGGL((gemv_kernel<FMT, NB, D, MT, false, PAIR, false>), dim3(grid), dim3(W * 64), lds, s, S, x,
+                           G, M, KCH, RPW, tpb);
+    }
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

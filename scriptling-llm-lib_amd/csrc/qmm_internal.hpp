@@ -92,18 +92,28 @@ sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, in
 // One GEMV launch over up to kMaxSegs weights of one format and one K that
 // share the activation rows x: weight i (N[i] rows) writes dst[i] (M x N[i]).
 constexpr int kMaxSegs = 4;
+// norm_w (optional): RMSNorm each activation row first (rmsNormFlatF32,
+// float32_ops.go:159-172, with weight vector norm_w and eps), fused into the
+// GEMV prologue.
 sllm_status launch_gemv_multi(int fmt, const Planes *P, float *const *dst, const int *N, int nseg,
-                              const float *x, int G, int M, hipStream_t s);
+                              const float *x, int G, int M, hipStream_t s, const float *norm_w = nullptr,
+                              float eps = 0.0f);
 // Paired gate / up GEMV of one FFN: h = SwiGLU(Wg x, Wu x) (model_f32.go:479-490);
 // gate / up (may be null) also receive the two matmul outputs. Both weights
 // have the same format, N rows and G blocks per row.
 sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, const float *x, float *h,
-                               float *gate, float *up, int N, int G, int M, hipStream_t s);
+                               float *gate, float *up, int N, int G, int M, hipStream_t s,
+                               const float *norm_w = nullptr, float eps = 0.0f);
 // One-row GEMV that also writes the greedy argmax of its outputs to *out
 // (device). logits may be null. key / cnt: 16 bytes of zeroed per-stream
 // scratch, left zeroed again by every launch.
 sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
-                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s);
+                               unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s,
+                               const float *norm_w = nullptr, float eps = 0.0f);
+// rmsNormFlatF32 of rows x K into out (the prefill path of the fused-norm
+// entry points; same statistics as the GEMV prologue).
+sllm_status launch_rmsnorm(const float *x, const float *norm_w, float eps, int rows, int K, float *out,
+                           hipStream_t s);
 // h[i] = SwiGLU(gate[i], up[i]) for n elements (the prefill path and mixed formats).
 sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s);
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,

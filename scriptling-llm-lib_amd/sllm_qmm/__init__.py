@@ -84,6 +84,10 @@ def lib() -> C.CDLL:
     L.sllm_matmul_swiglu_dev.argtypes = [W, W, P, i32, i32, P, P, P, P]
     L.sllm_matmul_argmax_dev.argtypes = [W, P, i32, P, P, P]
     L.sllm_matmul_argmax.argtypes = [W, P, C.POINTER(i32)]
+    f32 = C.c_float
+    L.sllm_rmsnorm_matmul_multi_dev.argtypes = [C.POINTER(W), i32, P, P, f32, i32, i32, C.POINTER(P), P]
+    L.sllm_rmsnorm_matmul_swiglu_dev.argtypes = [W, W, P, P, f32, i32, i32, P, P]
+    L.sllm_rmsnorm_matmul_argmax_dev.argtypes = [W, P, P, f32, i32, P, P, P]
     L.sllm_matmul_swiglu_into_f32.argtypes = [W, W, P, i32, i32, P]
     L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
@@ -301,6 +305,29 @@ def matmul_argmax_dev(w: DeviceWeight, x_ptr: int, argmax_ptr: int, logits_ptr: 
     """Device-resident head matmul + argmax: *argmax_ptr (device int32) gets the index."""
     _check(lib().sllm_matmul_argmax_dev(w.handle, C.c_void_p(x_ptr), w.cols, C.c_void_p(logits_ptr or None),
                                         C.c_void_p(argmax_ptr), C.c_void_p(stream)))
+
+
+def rmsnorm_matmul_multi_dev(ws: list, x_ptr: int, norm_w_ptr: int, eps: float, x_rows: int, x_cols: int,
+                             dst_ptrs: list, stream: int = 0) -> None:
+    """rmsNormFlatF32 + the layer's matmuls on the normed rows, one launch per format (decode)."""
+    hs = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+    ds = (C.c_void_p * len(ws))(*[C.c_void_p(p) for p in dst_ptrs])
+    _check(lib().sllm_rmsnorm_matmul_multi_dev(hs, len(ws), C.c_void_p(x_ptr), C.c_void_p(norm_w_ptr), eps,
+                                               x_rows, x_cols, ds, C.c_void_p(stream)))
+
+
+def rmsnorm_matmul_swiglu_dev(w_gate, w_up, x_ptr: int, norm_w_ptr: int, eps: float, x_rows: int, x_cols: int,
+                              h_ptr: int, stream: int = 0) -> None:
+    _check(lib().sllm_rmsnorm_matmul_swiglu_dev(w_gate.handle, w_up.handle, C.c_void_p(x_ptr),
+                                                C.c_void_p(norm_w_ptr), eps, x_rows, x_cols, C.c_void_p(h_ptr),
+                                                C.c_void_p(stream)))
+
+
+def rmsnorm_matmul_argmax_dev(w, x_ptr: int, norm_w_ptr: int, eps: float, argmax_ptr: int, logits_ptr: int = 0,
+                              stream: int = 0) -> None:
+    _check(lib().sllm_rmsnorm_matmul_argmax_dev(w.handle, C.c_void_p(x_ptr), C.c_void_p(norm_w_ptr), eps, w.cols,
+                                                C.c_void_p(logits_ptr or None), C.c_void_p(argmax_ptr),
+                                                C.c_void_p(stream)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

@@ -55,6 +55,8 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_matmul_swiglu_into_f32(None, None, p, 1, 32, p) == 1
     assert lib.sllm_matmul_argmax(None, p, C.byref(C.c_int())) == 1
     assert lib.sllm_matmul_argmax_dev(None, p, 32, None, p, None) == 1
+    assert lib.sllm_rmsnorm_matmul_argmax_dev(None, p, p, C.c_float(1e-5), 32, None, p, None) == 1
+    assert lib.sllm_rmsnorm_matmul_swiglu_dev(None, None, p, p, C.c_float(1e-5), 1, 32, p, None) == 1
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
