@@ -188,6 +188,80 @@ sllm_status sllm_rmsnorm_matmul_argmax_dev(const sllm_weight *w, const float *x_
                                            float eps, int x_cols, float *logits_dev, int *argmax_dev,
                                            void *stream);
 
+/*
+ * The matmul followed by the residual add: dst += x W^T (device buffers,
+ * dst x_rows x Rows). Replaces modelMatmulIntoF32(WO) + `xData[i] +=
+ * oData[i]` (model_f32.go:469-474) and modelMatmulIntoF32(WDown) + `xData[i]
+ * += downData[i]` (model_f32.go:492-497): the product is the one
+ * sllm_matmul_dev computes, then one float32 add per element, as in the
+ * reference. Decode adds in the GEMV's epilogue.
+ */
+sllm_status sllm_matmul_add_dev(const sllm_weight *w, const float *x_dev, int x_rows, int x_cols,
+                                float *dst_dev, void *stream);
+
+/* --------------------------------------------------------------------------
+ * The attention section of a step (forwardBlock, model_f32.go:398-466) on
+ * the device, with every layer's KV cache resident in HBM.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * KVCacheF32 (float32_ops.go:11-14) for n_layers layers: K and V rows of
+ * n_kv_heads heads, d_k floats each, up to max_seq positions per layer
+ * (InferenceModelF32.KVCaches, initKVCaches model_f32.go:310-318; the
+ * reference appends without bound, MaxSeqLen caps the context,
+ * model_f32.go:599-602). Layout: layer-major, then head, position, d_k
+ * (fp32, as the reference keeps it). d_k: a multiple of 4, at most 256.
+ */
+typedef struct sllm_kv_cache sllm_kv_cache;
+sllm_status sllm_kv_cache_create(int n_layers, int n_kv_heads, int d_k, int max_seq, sllm_kv_cache **out);
+void sllm_kv_cache_destroy(sllm_kv_cache *kv);
+/* Rows held by a layer (len(cache.K[h]) / dK in the reference). */
+sllm_status sllm_kv_cache_length(const sllm_kv_cache *kv, int layer, int *len);
+/* Every layer back to (or forward to) len rows: 0 starts a new sequence, as
+ * initKVCaches does when Generate starts at kvStartPos 0
+ * (model_f32.go:589-591). Rows beyond len keep their contents. */
+sllm_status sllm_kv_cache_set_length(sllm_kv_cache *kv, int len);
+/* Device addresses of layer's K and V (n_kv_heads x max_seq x d_k each). */
+sllm_status sllm_kv_cache_data(const sllm_kv_cache *kv, int layer, float **k_dev, float **v_dev);
+
+/* The model constants of the attention section (device pointers to the
+ * model's own tensors; NULL / 0 where the model has none). */
+typedef struct sllm_attn_params {
+    int n_heads;            /* m.nHeads */
+    int n_kv_heads;         /* m.nKVHeads (n_heads = n_kv_heads * nRep, nRep <= 8) */
+    int d_k;                /* m.dK */
+    int rope_half_dim;      /* m.ropeHalfDim (<= d_k / 2) */
+    const float *rope_freqs; /* m.ropeFreqs, rope_half_dim floats (model_f32.go:256-260) */
+    const float *q_bias;    /* block.QBias */
+    int q_bias_len;
+    const float *k_bias;    /* block.KBias */
+    int k_bias_len;
+    const float *v_bias;    /* block.VBias */
+    int v_bias_len;
+    const float *q_norm_w;  /* block.QNormW (d_k floats) */
+    const float *k_norm_w;  /* block.KNormW (d_k floats) */
+    float norm_eps;         /* Config.NormEps */
+} sllm_attn_params;
+
+/*
+ * forwardBlock's attention section for `layer` (model_f32.go:398-466): q_dev
+ * (seq_len x n_heads*d_k), k_dev and v_dev (seq_len x n_kv_heads*d_k) are the
+ * q/k/v matmul outputs. Adds the biases, RMSNorms each q / k head with
+ * QNormW / KNormW, applies RoPE at positions start_pos + r
+ * (applyRopeInPlaceF32, float32_ops.go:174-188), appends the k / v rows to
+ * the layer's cache, and writes the causal attention of every q head over
+ * the cache (q head h reads kv head h / nRep; fusedAttentionHeadF32,
+ * float32_ops.go:190-235) to out_dev, heads merged (seq_len x n_heads*d_k,
+ * mergeHeadsDataF32 float32_ops.go:262-273). q/k/v are not modified.
+ * Scores are the reference's sequential float32 dots; the softmax sums and
+ * the weighted sum of values are reassociated (split over the positions and
+ * combined), and the per-head RMSNorm sums its squares in the library's
+ * fixed order. Two launches; asynchronous on `stream`.
+ */
+sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q_dev,
+                               const float *k_dev, const float *v_dev, int seq_len, int start_pos,
+                               float *out_dev, void *stream);
+
 /* Host-buffer form of sllm_matmul_swiglu_dev (synchronous; h only). */
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,
                                         int x_rows, int x_cols, float *h);

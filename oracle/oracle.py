@@ -81,6 +81,10 @@ def lib() -> C.CDLL:
         L.ref_swiglu_n.argtypes = [P, P, P, i64]
         L.ref_rmsnorm.argtypes = [P, P, C.c_float, i32, i32, P]
         L.ref_rmsnorm_lib.argtypes = [P, P, C.c_float, i32, i32, P]
+        L.ref_rope.argtypes = [P, i32, i32, i32, P, i32]
+        L.ref_attention_head.argtypes = [P, P, P, i32, i32, i32, i32, i32, P, i32]
+        L.ref_attention_layer.argtypes = [P, P, P, i32, i32, i32, i32, P, i32, P, i32, P, i32, P, P,
+                                          C.c_float, i32, P, i32, i32, P, P, i32, i32, P, P]
         _lib = L
     return _lib
 
@@ -290,3 +294,58 @@ def baseline_time(qtype: str, raw: np.ndarray, N: int, x: np.ndarray, reps: int,
     raw = np.ascontiguousarray(raw, dtype=np.uint8)
     dst = np.empty((M, N), np.float32)
     return baseline().bl_time_matmul(qtype.encode(), _p(raw), N, K, _p(x), M, _p(dst), reps, trials)
+
+
+def _f32(a):
+    return None if a is None else np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _po(a):
+    return None if a is None else _p(a)
+
+
+def rope(data: np.ndarray, start_pos: int, freqs: np.ndarray, half_dim: int) -> np.ndarray:
+    """applyRopeInPlaceF32 (float32_ops.go:174-188) on a copy of data (rows x d_k)."""
+    out = np.array(data, dtype=np.float32, order="C", copy=True)
+    rows, d_k = out.shape
+    fr = _f32(freqs)
+    lib().ref_rope(_p(out), rows, d_k, start_pos, _p(fr), half_dim)
+    return out
+
+
+def attention_head(q, k, v, causal=True, cache_len=0) -> np.ndarray:
+    """fusedAttentionHeadF32 (float32_ops.go:190-235): q (q_rows x d_k) against
+    k / v (k_rows x d_k)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    out = np.zeros_like(q)
+    lib().ref_attention_head(_p(q), _p(k), _p(v), q.shape[0], q.shape[1], k.shape[0], int(causal), cache_len,
+                             _p(out), 0)
+    return out
+
+
+def attention_layer(q, k, v, n_heads, n_kv, d_k, cache_k, cache_v, cache_len, start_pos, freqs, half_dim,
+                    q_bias=None, k_bias=None, v_bias=None, q_norm_w=None, k_norm_w=None, eps=1e-5,
+                    lib_norm=False, return_q_rot=False):
+    """forwardBlock's attention section (model_f32.go:398-466) for one layer.
+
+    q: seq x n_heads*d_k, k / v: seq x n_kv*d_k (matmul outputs); cache_k /
+    cache_v: n_kv x cap x d_k holding cache_len rows per head. Returns (out
+    seq x n_heads*d_k, new cache_k, new cache_v[, q_rot: the normed, rotated q
+    heads, seq x n_heads*d_k]); the inputs are not modified.
+    """
+    q, k, v = (np.array(a, dtype=np.float32, order="C", copy=True) for a in (q, k, v))
+    ck = np.array(cache_k, dtype=np.float32, order="C", copy=True)
+    cv = np.array(cache_v, dtype=np.float32, order="C", copy=True)
+    seq = q.shape[0]
+    cap = ck.shape[1]
+    assert cache_len + seq <= cap
+    out = np.zeros((seq, n_heads * d_k), np.float32)
+    qr = np.zeros((seq, n_heads * d_k), np.float32)
+    qb, kb, vb = _f32(q_bias), _f32(k_bias), _f32(v_bias)
+    qn, kn, fr = _f32(q_norm_w), _f32(k_norm_w), _f32(freqs)
+    lib().ref_attention_layer(_p(q), _p(k), _p(v), seq, n_heads, n_kv, d_k,
+                              _po(qb), 0 if qb is None else qb.size, _po(kb), 0 if kb is None else kb.size,
+                              _po(vb), 0 if vb is None else vb.size, _po(qn), _po(kn), eps, int(lib_norm),
+                              _p(fr), half_dim, start_pos, _p(ck), _p(cv), cap, cache_len, _p(out),
+                              _p(qr) if return_q_rot else None)
+    return (out, ck, cv, qr) if return_q_rot else (out, ck, cv)

@@ -812,3 +812,127 @@ void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int co
         rms_apply(xr, w, ss, eps, cols, out + (size_t)r * cols);
     }
 }
+
+/* ---- the decode step around the matmuls --------------------------------- */
+
+/* applyRopeInPlaceF32, float32_ops.go:174-188. The angle is a float32
+ * product, cos / sin are taken in float64 and rounded to float32. */
+void ref_rope(float *data, int rows, int d_k, int start_pos, const float *freqs, int half_dim) {
+    for (int r = 0; r < rows; r++) {
+        const int pos = start_pos + r;
+        float *row = data + (size_t)r * d_k;
+        for (int i = 0; i < half_dim; i++) {
+            const float angle = freqs[i] * (float)pos;
+            const float c = (float)cos((double)angle);
+            const float s = (float)sin((double)angle);
+            const float x0 = row[2 * i], x1 = row[2 * i + 1];
+            row[2 * i] = x0 * c - x1 * s;
+            row[2 * i + 1] = x0 * s + x1 * c;
+        }
+    }
+}
+
+/* fusedAttentionHeadF32, float32_ops.go:190-235: sequential float32 dot,
+ * scale, causal -Inf mask, max (first score, then strict >), float32(exp(
+ * float64(score - max))), sequential float32 sum, invSum = 1 / sum, and
+ * out[d] = sum over ki of (exps[ki] * invSum) * v[ki][d], sequentially. */
+void ref_attention_head(const float *q, const float *k, const float *v, int q_rows, int d_k, int k_rows,
+                        int causal, int cache_len, float *out, int out_off) {
+    const float scale = 1.0f / (float)sqrt((double)d_k);
+    float *scores = (float *)malloc(sizeof(float) * (size_t)(k_rows > 0 ? k_rows : 1));
+    float *exps = (float *)malloc(sizeof(float) * (size_t)(k_rows > 0 ? k_rows : 1));
+    for (int qi = 0; qi < q_rows; qi++) {
+        const float *qr = q + (size_t)qi * d_k;
+        for (int ki = 0; ki < k_rows; ki++) {
+            const float *kr = k + (size_t)ki * d_k;
+            float dot = 0.0f;
+            for (int d = 0; d < d_k; d++) dot += qr[d] * kr[d];
+            scores[ki] = dot * scale;
+        }
+        if (causal) {
+            for (int ki = cache_len + qi + 1; ki < k_rows; ki++) scores[ki] = -INFINITY;
+        }
+        float mx = scores[0];
+        for (int ki = 1; ki < k_rows; ki++)
+            if (scores[ki] > mx) mx = scores[ki];
+        float sum = 0.0f;
+        for (int ki = 0; ki < k_rows; ki++) {
+            const float e = (float)exp((double)(scores[ki] - mx));
+            exps[ki] = e;
+            sum += e;
+        }
+        const float inv = 1.0f / sum;
+        float *o = out + out_off + (size_t)qi * d_k;
+        for (int d = 0; d < d_k; d++) {
+            float val = 0.0f;
+            for (int ki = 0; ki < k_rows; ki++) {
+                const float t = exps[ki] * inv;
+                val += t * v[(size_t)ki * d_k + d];
+            }
+            o[d] = val;
+        }
+    }
+    free(scores);
+    free(exps);
+}
+
+/* forwardBlock, model_f32.go:398-466: bias adds (:398-420), splitHeadsDataF32
+ * (float32_ops.go:237-250), per-head QK RMSNorm (:424-435), RoPE (:437-443),
+ * KV append (:445-448), repeatKVDataF32 (float32_ops.go:252-260: q head h reads kv head h / nRep,
+ * :455-458), fusedAttentionHeadF32 with causal masking (:460-466) and
+ * mergeHeadsDataF32 (float32_ops.go:262-273). */
+void ref_attention_layer(float *q, float *k, float *v, int seq_len, int n_heads, int n_kv, int d_k,
+                         const float *q_bias, int q_bias_len, const float *k_bias, int k_bias_len,
+                         const float *v_bias, int v_bias_len, const float *q_norm_w, const float *k_norm_w,
+                         float eps, int lib_norm, const float *freqs, int half_dim, int start_pos,
+                         float *cache_k, float *cache_v, int cap, int cache_len, float *out, float *q_rot) {
+    const int qc = n_heads * d_k, kc = n_kv * d_k;
+    for (int s = 0; s < seq_len; s++) {
+        if (q_bias)
+            for (int j = 0; j < q_bias_len && j < qc; j++) q[(size_t)s * qc + j] += q_bias[j];
+        if (k_bias)
+            for (int j = 0; j < k_bias_len && j < kc; j++) k[(size_t)s * kc + j] += k_bias[j];
+        if (v_bias)
+            for (int j = 0; j < v_bias_len && j < kc; j++) v[(size_t)s * kc + j] += v_bias[j];
+    }
+    const size_t hs = (size_t)seq_len * d_k;
+    float *qh = (float *)malloc(sizeof(float) * hs * (size_t)n_heads);
+    float *kh = (float *)malloc(sizeof(float) * hs * (size_t)n_kv);
+    float *vh = (float *)malloc(sizeof(float) * hs * (size_t)n_kv);
+    for (int s = 0; s < seq_len; s++) {
+        for (int h = 0; h < n_heads; h++)
+            memcpy(qh + h * hs + (size_t)s * d_k, q + (size_t)s * qc + (size_t)h * d_k, sizeof(float) * d_k);
+        for (int g = 0; g < n_kv; g++) {
+            memcpy(kh + g * hs + (size_t)s * d_k, k + (size_t)s * kc + (size_t)g * d_k, sizeof(float) * d_k);
+            memcpy(vh + g * hs + (size_t)s * d_k, v + (size_t)s * kc + (size_t)g * d_k, sizeof(float) * d_k);
+        }
+    }
+    void (*norm)(const float *, const float *, float, int, int, float *) = lib_norm ? ref_rmsnorm_lib : ref_rmsnorm;
+    if (q_norm_w)
+        for (int h = 0; h < n_heads; h++) norm(qh + h * hs, q_norm_w, eps, seq_len, d_k, qh + h * hs);
+    if (k_norm_w)
+        for (int g = 0; g < n_kv; g++) norm(kh + g * hs, k_norm_w, eps, seq_len, d_k, kh + g * hs);
+    for (int h = 0; h < n_heads; h++) ref_rope(qh + h * hs, seq_len, d_k, start_pos, freqs, half_dim);
+    for (int g = 0; g < n_kv; g++) ref_rope(kh + g * hs, seq_len, d_k, start_pos, freqs, half_dim);
+    for (int g = 0; g < n_kv; g++) {
+        memcpy(cache_k + ((size_t)g * cap + cache_len) * d_k, kh + g * hs, sizeof(float) * hs);
+        memcpy(cache_v + ((size_t)g * cap + cache_len) * d_k, vh + g * hs, sizeof(float) * hs);
+    }
+    const int kv_len = cache_len + seq_len, rep = n_heads / n_kv;
+    float *att = (float *)malloc(sizeof(float) * hs * (size_t)n_heads);
+    for (int h = 0; h < n_heads; h++) {
+        const int g = h / rep;
+        ref_attention_head(qh + h * hs, cache_k + (size_t)g * cap * d_k, cache_v + (size_t)g * cap * d_k, seq_len,
+                           d_k, kv_len, 1, cache_len, att, (int)(h * hs));
+    }
+    for (int s = 0; s < seq_len; s++)
+        for (int h = 0; h < n_heads; h++) {
+            memcpy(out + (size_t)s * qc + (size_t)h * d_k, att + h * hs + (size_t)s * d_k, sizeof(float) * d_k);
+            if (q_rot)
+                memcpy(q_rot + (size_t)s * qc + (size_t)h * d_k, qh + h * hs + (size_t)s * d_k, sizeof(float) * d_k);
+        }
+    free(qh);
+    free(kh);
+    free(vh);
+    free(att);
+}

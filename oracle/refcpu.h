@@ -20,15 +20,6 @@
 
 #ifdef __cplusplus
 extern "C" {
-/* model_f32.go:486-489 SwiGLU, one element and n elements. */
-float ref_swiglu(float gate, float up);
-void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
-
-/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
- * the library's sum-of-squares association. */
-void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
-void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
-
 #endif
 
 /* ---- f16 codecs -------------------------------------------------------- */
@@ -107,25 +98,44 @@ int ref_argmax(const float *v, int n);
 /* Bytes per 32-element block of a QType's Raw ("q5k1" counts both halves). */
 int ref_block_bytes(const char *qtype);
 
+/* model_f32.go:486-489 SwiGLU, one element and n elements. */
+float ref_swiglu(float gate, float up);
+void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
+
+/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
+ * the library's sum-of-squares association. */
+void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
+void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
+
+/* ---- the decode step around the matmuls --------------------------------- */
+/* applyRopeInPlaceF32 (float32_ops.go:174-188): rows x d_k, pairs (2i, 2i+1),
+ * i < half_dim, at positions start_pos + r. */
+void ref_rope(float *data, int rows, int d_k, int start_pos, const float *freqs, int half_dim);
+/* fusedAttentionHeadF32 (float32_ops.go:190-235): q q_rows x d_k, k / v
+ * k_rows x d_k; out rows at out + out_off. */
+void ref_attention_head(const float *q, const float *k, const float *v, int q_rows, int d_k, int k_rows,
+                        int causal, int cache_len, float *out, int out_off);
+/*
+ * forwardBlock's attention section (model_f32.go:398-466) for one layer:
+ * q / k / v are the matmul outputs (seq_len x n_heads*d_k, seq_len x
+ * n_kv*d_k); bias vectors (length q_bias_len ... or NULL), per-head QK RMSNorm
+ * weights (d_k, or NULL; lib_norm: the library's sum-of-squares association),
+ * RoPE at start_pos, then the rows are appended to the cache (cache_k /
+ * cache_v: n_kv x cap x d_k, holding cache_len rows per head) and the causal
+ * GQA attention of every head is written merged (seq_len x n_heads*d_k).
+ * The bias adds modify q, k and v in place, as the reference's do; the
+ * normed and rotated heads are copies, as the reference's split heads are.
+ * q_rot (or NULL) receives the normed, rotated q heads (seq_len x
+ * n_heads*d_k).
+ */
+void ref_attention_layer(float *q, float *k, float *v, int seq_len, int n_heads, int n_kv, int d_k,
+                         const float *q_bias, int q_bias_len, const float *k_bias, int k_bias_len,
+                         const float *v_bias, int v_bias_len, const float *q_norm_w, const float *k_norm_w,
+                         float eps, int lib_norm, const float *freqs, int half_dim, int start_pos,
+                         float *cache_k, float *cache_v, int cap, int cache_len, float *out, float *q_rot);
+
 #ifdef __cplusplus
 }
-/* model_f32.go:486-489 SwiGLU, one element and n elements. */
-float ref_swiglu(float gate, float up);
-void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
-
-/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
- * the library's sum-of-squares association. */
-void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
-void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
-
 #endif
-/* model_f32.go:486-489 SwiGLU, one element and n elements. */
-float ref_swiglu(float gate, float up);
-void ref_swiglu_n(const float *gate, const float *up, float *h, int64_t n);
-
-/* rmsNormFlatF32 (float32_ops.go:159-172) in the reference's order, and with
- * the library's sum-of-squares association. */
-void ref_rmsnorm(const float *x, const float *w, float eps, int rows, int cols, float *out);
-void ref_rmsnorm_lib(const float *x, const float *w, float eps, int rows, int cols, float *out);
 
 #endif

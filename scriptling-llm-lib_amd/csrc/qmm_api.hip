@@ -2,6 +2,7 @@
 // stand in for the reference's Go matmul functions, and verification hooks.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <mutex>
@@ -18,6 +19,15 @@ struct sllm_weight {
     void *base = nullptr;
     size_t bytes = 0;
     sllm::MutPlanes planes;
+};
+
+// KVCacheF32 (float32_ops.go:11-14) of every layer on the device: K and V of
+// layer l, kv head g, position p at ((l * n_kv + g) * cap + p) * d_k.
+struct sllm_kv_cache {
+    int n_layers = 0, n_kv = 0, d_k = 0, cap = 0;
+    int device = 0;
+    float *k = nullptr, *v = nullptr;
+    std::vector<int> len;  // rows held per layer
 };
 
 namespace sllm {
@@ -72,6 +82,43 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
         SLLM_HIP(hipMemsetAsync(p, 0, 64, stream));
     }
     *out = p;
+    return SLLM_OK;
+}
+
+// Attention split counters per (device, stream): zeroed when allocated, left
+// zeroed by every attention launch.
+struct Cnt {
+    unsigned int *p = nullptr;
+    size_t n = 0;
+};
+std::unordered_map<uint64_t, Cnt> g_attn_cnt;
+
+sllm_status attn_counters(hipStream_t stream, size_t n, unsigned int **out) {
+    int dev = 0;
+    SLLM_HIP(hipGetDevice(&dev));
+    const uint64_t key = ((uint64_t)(uintptr_t)stream << 8) ^ (uint64_t)dev;
+    std::lock_guard<std::mutex> lk(g_mu);
+    Cnt &c = g_attn_cnt[key];
+    if (c.n < n) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+            return set_error(SLLM_ERR_ARG, "attention: this call would allocate counters on a capturing stream; "
+                                           "make a call with as many rows on the stream before capturing it");
+        if (c.p) {
+            SLLM_HIP(hipStreamSynchronize(stream));
+            (void)hipFree(c.p);
+            c.p = nullptr;
+            c.n = 0;
+        }
+        const size_t want = n < 4096 ? 4096 : n;
+        if (hipMalloc(&c.p, want * sizeof(unsigned int)) != hipSuccess) {
+            c.p = nullptr;
+            return set_error(SLLM_ERR_OOM, "attention counter allocation failed");
+        }
+        c.n = want;
+        SLLM_HIP(hipMemsetAsync(c.p, 0, want * sizeof(unsigned int), stream));
+    }
+    *out = c.p;
     return SLLM_OK;
 }
 
@@ -862,6 +909,160 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
     release(c);
     if (e != hipSuccess) return hip_error(e, "debug_block_dots");
     return st;
+}
+
+sllm_status sllm_matmul_add_dev(const sllm_weight *w, const float *x, int x_rows, int x_cols, float *dst,
+                                void *stream) {
+    if (!w || !x || !dst) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0) return set_error(SLLM_ERR_ARG, "xRows must be positive");
+    if (x_cols != w->cols) return set_error(SLLM_ERR_ARG, "xCols does not match the weight's Cols");
+    if (((uintptr_t)x & 15) != 0) return set_error(SLLM_ERR_ARG, "x must be 16-byte aligned");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    const Planes P = as_const(w->planes);
+    if (!uses_gemm(w, x_rows)) return launch_gemv_add(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    // GEMM: the product into the workspace behind the GEMM's own, then dst += it
+    const size_t gb = align256(gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows));
+    const size_t n = (size_t)x_rows * w->rows;
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, gb + n * sizeof(float), &ws, &cap)) != SLLM_OK) return st;
+    float *tmp = (float *)((char *)ws + gb);
+    if ((st = launch_gemm(w->fmt, P, x, tmp, w->rows, w->groups, x_rows, ws, gb, s)) != SLLM_OK) return st;
+    return launch_add(dst, tmp, n, s);
+}
+
+sllm_status sllm_kv_cache_create(int n_layers, int n_kv_heads, int d_k, int max_seq, sllm_kv_cache **out) {
+    if (!out) return set_error(SLLM_ERR_ARG, "null pointer");
+    *out = nullptr;
+    if (n_layers <= 0 || n_kv_heads <= 0 || max_seq <= 0 || d_k <= 0)
+        return set_error(SLLM_ERR_ARG, "KV cache dimensions must be positive");
+    if (d_k % 4 != 0 || d_k > 256) return set_error(SLLM_ERR_SHAPE, "d_k must be a multiple of 4, at most 256");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    auto *kv = new sllm_kv_cache();
+    kv->n_layers = n_layers;
+    kv->n_kv = n_kv_heads;
+    kv->d_k = d_k;
+    kv->cap = max_seq;
+    kv->len.assign((size_t)n_layers, 0);
+    (void)hipGetDevice(&kv->device);
+    const size_t bytes = (size_t)n_layers * n_kv_heads * max_seq * d_k * sizeof(float);
+    if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess) {
+        (void)hipFree(kv->k);
+        (void)hipFree(kv->v);
+        delete kv;
+        return set_error(SLLM_ERR_OOM, "KV cache allocation failed");
+    }
+    hipError_t e = hipMemsetAsync(kv->k, 0, bytes, nullptr);
+    if (e == hipSuccess) e = hipMemsetAsync(kv->v, 0, bytes, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        (void)hipFree(kv->k);
+        (void)hipFree(kv->v);
+        delete kv;
+        return hip_error(e, "KV cache clear");
+    }
+    *out = kv;
+    return SLLM_OK;
+}
+
+void sllm_kv_cache_destroy(sllm_kv_cache *kv) {
+    if (!kv) return;
+    (void)hipFree(kv->k);
+    (void)hipFree(kv->v);
+    delete kv;
+}
+
+sllm_status sllm_kv_cache_length(const sllm_kv_cache *kv, int layer, int *len) {
+    if (!kv || !len) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
+    *len = kv->len[(size_t)layer];
+    return SLLM_OK;
+}
+
+sllm_status sllm_kv_cache_set_length(sllm_kv_cache *kv, int len) {
+    if (!kv) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (len < 0 || len > kv->cap) return set_error(SLLM_ERR_ARG, "length outside 0 .. max_seq");
+    for (int &l : kv->len) l = len;
+    return SLLM_OK;
+}
+
+sllm_status sllm_kv_cache_data(const sllm_kv_cache *kv, int layer, float **k_dev, float **v_dev) {
+    if (!kv || !k_dev || !v_dev) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
+    const size_t off = (size_t)layer * kv->n_kv * kv->cap * kv->d_k;
+    *k_dev = kv->k + off;
+    *v_dev = kv->v + off;
+    return SLLM_OK;
+}
+
+sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q,
+                               const float *k, const float *v, int seq_len, int start_pos, float *out,
+                               void *stream) {
+    if (!kv || !p || !q || !k || !v || !out) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
+    if (seq_len <= 0) return set_error(SLLM_ERR_ARG, "seq_len must be positive");
+    if (start_pos < 0) return set_error(SLLM_ERR_ARG, "start_pos must not be negative");
+    if (p->n_kv_heads != kv->n_kv || p->d_k != kv->d_k)
+        return set_error(SLLM_ERR_ARG, "n_kv_heads / d_k differ from the KV cache's");
+    if (p->n_heads <= 0 || p->n_heads % p->n_kv_heads != 0 || p->n_heads / p->n_kv_heads > 8)
+        return set_error(SLLM_ERR_SHAPE, "n_heads must be a multiple of n_kv_heads, at most 8 times it");
+    if (p->rope_half_dim < 0 || 2 * p->rope_half_dim > p->d_k)
+        return set_error(SLLM_ERR_ARG, "rope_half_dim outside 0 .. d_k / 2");
+    if (p->rope_half_dim > 0 && !p->rope_freqs) return set_error(SLLM_ERR_ARG, "null rope_freqs");
+    if (p->q_bias_len < 0 || p->k_bias_len < 0 || p->v_bias_len < 0)
+        return set_error(SLLM_ERR_ARG, "negative bias length");
+    const int cl = kv->len[(size_t)layer];
+    if ((int64_t)cl + seq_len > kv->cap) return set_error(SLLM_ERR_SHAPE, "KV cache full (max_seq rows)");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    hipStream_t s = (hipStream_t)stream;
+    int splits = 0, tps = 0;
+    size_t wsb = 0;
+    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &wsb);
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
+    unsigned int *cnt = nullptr;
+    if ((st = attn_counters(s, (size_t)seq_len * kv->n_kv, &cnt)) != SLLM_OK) return st;
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.seq = seq_len;
+    a.n_heads = p->n_heads;
+    a.n_kv = kv->n_kv;
+    a.d_k = kv->d_k;
+    a.rep = p->n_heads / kv->n_kv;
+    a.q_bias = p->q_bias_len ? p->q_bias : nullptr;
+    a.k_bias = p->k_bias_len ? p->k_bias : nullptr;
+    a.v_bias = p->v_bias_len ? p->v_bias : nullptr;
+    a.qb_len = p->q_bias_len;
+    a.kb_len = p->k_bias_len;
+    a.vb_len = p->v_bias_len;
+    a.q_norm = p->q_norm_w;
+    a.k_norm = p->k_norm_w;
+    a.eps = p->norm_eps;
+    a.freqs = p->rope_freqs;
+    a.half_dim = p->rope_half_dim;
+    a.start_pos = start_pos;
+    const size_t loff = (size_t)layer * kv->n_kv * kv->cap * kv->d_k;
+    a.cache_k = kv->k + loff;
+    a.cache_v = kv->v + loff;
+    a.cap = kv->cap;
+    a.cache_len = cl;
+    a.scale = 1.0f / (float)std::sqrt((double)kv->d_k);  // fusedAttentionHeadF32, float32_ops.go:191
+    a.out = out;
+    a.qrot = (float *)ws;
+    a.part = (float *)((char *)ws + align256((size_t)seq_len * p->n_heads * kv->d_k * sizeof(float)));
+    a.cnt = cnt;
+    a.splits = splits;
+    a.tps = tps;
+    if ((st = launch_attention(a, s)) != SLLM_OK) return st;
+    kv->len[(size_t)layer] = cl + seq_len;
+    return SLLM_OK;
 }
 
 }  // extern "C"

@@ -216,6 +216,29 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
     return sum;
 }
 
+// ------------------------------------------------------ wave reduction ----
+
+// Sum over the 64 lanes of a wave with DPP moves (no LDS round trips), in a
+// fixed order: pairs, quads, 8-lane and 16-lane rows within each row of 16
+// lanes, then the four row sums (lanes 0, 16, 32, 48) added left to right.
+// Every lane receives the result.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    const int m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
+    return v + __builtin_bit_cast(float, m);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+    v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of each 8 lanes
+    v = dpp_add<0x140>(v);  // row_mirror: the other 8 lanes of each row of 16
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return ((r0 + r1) + r2) + r3;
+}
+
 // Padded LDS stride (floats) of one 32-element fp32 activation block, chosen so
 // that 16 lanes reading 16 B from consecutive blocks hit distinct banks.
 constexpr int kXfStride = 36;

@@ -59,7 +59,7 @@ namespace {
 sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const int *N, int nseg, bool pair,
                             const float *x, int G, int M, hipStream_t s, const float *norm_w, float eps,
                             unsigned long long *amax_key = nullptr, unsigned int *amax_cnt = nullptr,
-                            int *amax_out = nullptr) {
+                            int *amax_out = nullptr, bool accum = false) {
     if (nseg < 1 || nseg > kMaxSegs) return set_error(SLLM_ERR_ARG, "gemv: 1 to 4 weights per launch");
     if (G <= 0 || M <= 0) return set_error(SLLM_ERR_ARG, "gemv: empty shape");
     if (pair && (nseg != 2 || N[0] != N[1])) return set_error(SLLM_ERR_ARG, "gemv: gate / up shapes differ");
@@ -116,6 +116,7 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     S.amax_key = amax_key;
     S.amax_cnt = amax_cnt;
     S.amax_out = amax_out;
+    S.accum = accum ? 1 : 0;
     S.norm_w = norm_w;
     S.norm_eps = eps;
     S.wave0[0] = 0;
@@ -187,6 +188,12 @@ sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, cons
 sllm_status launch_gemv(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         hipStream_t s) {
     return launch_gemv_multi(fmt, &P, &dst, &N, 1, x, G, M, s);
+}
+
+sllm_status launch_gemv_add(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                            hipStream_t s) {
+    return plan_and_launch(fmt, &P, &dst, &N, 1, false, x, G, M, s, nullptr, 0.0f, nullptr, nullptr, nullptr,
+                           true);
 }
 
 sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
@@ -357,6 +364,10 @@ __global__ void swiglu_kernel(const float *__restrict__ gate, const float *__res
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
         h[i] = swiglu(gate[i], up[i]);
 }
+__global__ void add_kernel(float *__restrict__ dst, const float *__restrict__ src, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = dst[i] + src[i];
+}
 }  // namespace
 
 sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s) {
@@ -364,6 +375,14 @@ sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n
     const size_t blocks = (n + 255) / 256;
     hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, gate, up,
                        h, n);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
+}
+
+sllm_status launch_add(float *dst, const float *src, size_t n, hipStream_t s) {
+    if (n == 0) return SLLM_OK;
+    const size_t blocks = (n + 255) / 256;
+    hipLaunchKernelGGL(add_kernel, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, dst, src, n);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

@@ -190,26 +190,6 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
     }
 }
 
-// Sum over the 64 lanes of a wave with DPP moves (no LDS round trips), in a
-// fixed order: pairs, quads, 8-lane and 16-lane rows within each row of 16
-// lanes, then the four row sums (lanes 0, 16, 32, 48) added left to right.
-// Every lane receives the result.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-    const int m = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false);
-    return v + __builtin_bit_cast(float, m);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-    v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
-    v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]: lane ^ 2
-    v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of each 8 lanes
-    v = dpp_add<0x140>(v);  // row_mirror: the other 8 lanes of each row of 16
-    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
-    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
-    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
-    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
-    return ((r0 + r1) + r2) + r3;
-}
 
 template <int FMT, int NB, int D, int TPB, class Issue>
 __device__ __forceinline__ void prologue(BlockRegs (&buf)[D][NB], const float *__restrict__ x, int M, int G,
@@ -358,6 +338,7 @@ struct SegTable {
     unsigned long long *amax_key;
     unsigned int *amax_cnt;  // [0] workgroups done, [1] row 0 is NaN
     int *amax_out;
+    int accum;  // non-zero: dst += result (the residual add after o / down)
 };
 
 // Order-preserving key of a non-NaN value and its row: larger values give
@@ -597,7 +578,8 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
                 if (S.dst[1]) S.dst[1][o] = g;
                 if (S.dst[2]) S.dst[2][o] = u;
             } else if (dst) {
-                dst[o] = res[m];
+                // model_f32.go:472-474 / 495-497: x[i] += o[i], one float32 add
+                dst[o] = S.accum ? dst[o] + res[m] : res[m];
             }
         }
     }

@@ -110,6 +110,12 @@ sllm_status launch_gemv_swiglu(int fmt, const Planes &Pg, const Planes &Pu, cons
 sllm_status launch_gemv_argmax(int fmt, const Planes &P, const float *x, float *logits, int N, int G,
                                unsigned long long *key, unsigned int *cnt, int *out, hipStream_t s,
                                const float *norm_w = nullptr, float eps = 0.0f);
+// dst (M x N) += the GEMV's result: the residual add that follows the o and
+// down matmuls (model_f32.go:472-474, 495-497), in the GEMV epilogue.
+sllm_status launch_gemv_add(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                            hipStream_t s);
+// dst[i] += src[i] for n elements (the GEMM path of the residual add).
+sllm_status launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 // rmsNormFlatF32 of rows x K into out (the prefill path of the fused-norm
 // entry points; same statistics as the GEMV prologue).
 sllm_status launch_rmsnorm(const float *x, const float *norm_w, float eps, int rows, int K, float *out,
@@ -132,6 +138,31 @@ sllm_status pack_from_raw(int fmt, const uint8_t *raw_dev, int rows, int G, cons
 sllm_status pack_from_gguf(uint32_t ggml_type, const uint8_t *raw_dev, int rows, int cols,
                            const MutPlanes &P, hipStream_t s);
 sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
+
+// The attention section of one layer (forwardBlock, model_f32.go:398-466) on
+// device buffers; launch_attention checks nothing (the C entry does).
+struct AttnArgs {
+    const float *q, *k, *v;  // matmul outputs: seq x n_heads*d_k, seq x n_kv*d_k
+    int seq, n_heads, n_kv, d_k, rep;
+    const float *q_bias, *k_bias, *v_bias;  // or null
+    int qb_len, kb_len, vb_len;
+    const float *q_norm, *k_norm;  // per-head RMSNorm weights (d_k) or null
+    float eps;
+    const float *freqs;  // RoPE frequencies (half_dim)
+    int half_dim, start_pos;
+    float *cache_k, *cache_v;  // this layer: n_kv x cap x d_k
+    int cap, cache_len;        // rows held before this call
+    float scale;               // 1 / float32(sqrt(float64(d_k)))
+    float *out;                // seq x n_heads*d_k (merged heads)
+    float *qrot;               // workspace: seq x n_heads x d_k
+    float *part;               // workspace: seq x n_heads x splits x (d_k + 2)
+    unsigned int *cnt;         // seq x n_kv counters, zero before and after each launch
+    int splits, tps;           // splits per (row, kv head); tiles of 64 positions per split
+};
+// Split plan and workspace bytes (qrot + partials) of an attention call.
+void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps,
+                    size_t *ws_bytes);
+sllm_status launch_attention(const AttnArgs &a, hipStream_t s);
 
 // Tuning parameters (launch shapes), settable through sllm_set_param.
 struct Tuning {

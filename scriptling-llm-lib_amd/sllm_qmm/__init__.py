@@ -52,6 +52,15 @@ class SllmError(RuntimeError):
 _lib = None
 
 
+class AttnParams(C.Structure):
+    """sllm_attn_params: the model constants of the attention section (device
+    pointers to the model's tensors, 0 / None where the model has none)."""
+    _fields_ = [("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("d_k", C.c_int), ("rope_half_dim", C.c_int),
+                ("rope_freqs", C.c_void_p), ("q_bias", C.c_void_p), ("q_bias_len", C.c_int),
+                ("k_bias", C.c_void_p), ("k_bias_len", C.c_int), ("v_bias", C.c_void_p), ("v_bias_len", C.c_int),
+                ("q_norm_w", C.c_void_p), ("k_norm_w", C.c_void_p), ("norm_eps", C.c_float)]
+
+
 def lib() -> C.CDLL:
     """Load libsllm_qmm.so (raises if it has not been built)."""
     global _lib
@@ -93,11 +102,18 @@ def lib() -> C.CDLL:
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
     L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
     L.sllm_set_param.argtypes = [C.c_char_p, i32]
+    L.sllm_matmul_add_dev.argtypes = [W, P, i32, i32, P, P]
+    L.sllm_kv_cache_create.argtypes = [i32, i32, i32, i32, C.POINTER(P)]
+    L.sllm_kv_cache_destroy.argtypes = [P]
+    L.sllm_kv_cache_length.argtypes = [P, i32, C.POINTER(i32)]
+    L.sllm_kv_cache_set_length.argtypes = [P, i32]
+    L.sllm_kv_cache_data.argtypes = [P, i32, C.POINTER(P), C.POINTER(P)]
+    L.sllm_attention_dev.argtypes = [P, i32, C.POINTER(AttnParams), P, P, P, i32, i32, P, P]
     for name in exported_names():  # raises AttributeError if a declared symbol is missing
         f = getattr(L, name)
         if name in ("sllm_last_error", "sllm_kernel_info"):
             f.restype = C.c_char_p
-        elif name == "sllm_weight_destroy":
+        elif name in ("sllm_weight_destroy", "sllm_kv_cache_destroy"):
             f.restype = None
         else:
             f.restype = i32
@@ -328,6 +344,58 @@ def rmsnorm_matmul_argmax_dev(w, x_ptr: int, norm_w_ptr: int, eps: float, argmax
     _check(lib().sllm_rmsnorm_matmul_argmax_dev(w.handle, C.c_void_p(x_ptr), C.c_void_p(norm_w_ptr), eps, w.cols,
                                                 C.c_void_p(logits_ptr or None), C.c_void_p(argmax_ptr),
                                                 C.c_void_p(stream)))
+
+
+def matmul_add_dev(w: DeviceWeight, x_ptr: int, x_rows: int, x_cols: int, dst_ptr: int, stream: int = 0) -> None:
+    """dst += x W^T on device buffers: the o / down matmul with the residual add
+    that follows it (model_f32.go:469-474, 492-497)."""
+    _check(lib().sllm_matmul_add_dev(w.handle, C.c_void_p(x_ptr), x_rows, x_cols, C.c_void_p(dst_ptr),
+                                     C.c_void_p(stream)))
+
+
+class KVCache:
+    """KVCacheF32 (float32_ops.go:11-14) of every layer, resident in device
+    memory: n_kv_heads x max_seq x d_k floats of K and of V per layer."""
+
+    def __init__(self, n_layers: int, n_kv_heads: int, d_k: int, max_seq: int):
+        h = C.c_void_p()
+        _check(lib().sllm_kv_cache_create(n_layers, n_kv_heads, d_k, max_seq, C.byref(h)))
+        self.handle = h
+        self.n_layers, self.n_kv_heads, self.d_k, self.max_seq = n_layers, n_kv_heads, d_k, max_seq
+
+    def close(self) -> None:
+        if self.handle:
+            lib().sllm_kv_cache_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def length(self, layer: int) -> int:
+        n = C.c_int()
+        _check(lib().sllm_kv_cache_length(self.handle, layer, C.byref(n)))
+        return n.value
+
+    def set_length(self, n: int) -> None:
+        _check(lib().sllm_kv_cache_set_length(self.handle, n))
+
+    def data(self, layer: int) -> tuple[int, int]:
+        k, v = C.c_void_p(), C.c_void_p()
+        _check(lib().sllm_kv_cache_data(self.handle, layer, C.byref(k), C.byref(v)))
+        return k.value, v.value
+
+
+def attention_dev(kv: KVCache, layer: int, params: AttnParams, q_ptr: int, k_ptr: int, v_ptr: int, seq_len: int,
+                  start_pos: int, out_ptr: int, stream: int = 0) -> None:
+    """forwardBlock's attention section for one layer (model_f32.go:398-466):
+    bias, QK norm, RoPE at start_pos, KV append, causal GQA attention, merged
+    heads into out (seq_len x n_heads*d_k)."""
+    _check(lib().sllm_attention_dev(kv.handle, layer, C.byref(params), C.c_void_p(q_ptr), C.c_void_p(k_ptr),
+                                    C.c_void_p(v_ptr), seq_len, start_pos, C.c_void_p(out_ptr),
+                                    C.c_void_p(stream)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

@@ -57,6 +57,16 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_matmul_argmax_dev(None, p, 32, None, p, None) == 1
     assert lib.sllm_rmsnorm_matmul_argmax_dev(None, p, p, C.c_float(1e-5), 32, None, p, None) == 1
     assert lib.sllm_rmsnorm_matmul_swiglu_dev(None, None, p, p, C.c_float(1e-5), 1, 32, p, None) == 1
+    assert lib.sllm_matmul_add_dev(None, p, 1, 32, p, None) == 1
+    kv = C.c_void_p()
+    assert lib.sllm_kv_cache_create(0, 8, 128, 16, C.byref(kv)) == 1                      # no layers
+    assert lib.sllm_kv_cache_create(2, 8, 130, 16, C.byref(kv)) == 3                      # d_k % 4
+    assert lib.sllm_kv_cache_create(2, 8, 512, 16, C.byref(kv)) == 3                      # d_k > 256
+    assert lib.sllm_kv_cache_length(None, 0, C.byref(C.c_int())) == 1
+    assert lib.sllm_kv_cache_set_length(None, 0) == 1
+    prm = sq.AttnParams(n_heads=32, n_kv_heads=8, d_k=128, rope_half_dim=64)
+    assert lib.sllm_attention_dev(None, 0, C.byref(prm), p, p, p, 1, 0, p, None) == 1
+    lib.sllm_kv_cache_destroy(None)                                                        # no-op
 
 
 @pytest.mark.skipif(os.path.exists("/dev/kfd"), reason="checks the no-GPU error path")
@@ -76,5 +86,6 @@ def test_python_host_mirror_names():
     # the Go entry points this path replaces, mirrored by the host module
     for name in ("QuantWeight", "load_weight_f32_direct", "quantize_q8_rows_f32",
                  "model_matmul_quant_into_f32", "model_matmul_row_quant_into_f32", "argmax_f32_dev",
-                 "model_matmul_multi_quant_into_f32", "model_matmul_swiglu_into_f32", "matmul_argmax"):
+                 "model_matmul_multi_quant_into_f32", "model_matmul_swiglu_into_f32", "matmul_argmax",
+                 "KVCache", "attention_dev", "matmul_add_dev"):
         assert hasattr(sq, name)
