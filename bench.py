@@ -442,6 +442,8 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     ms_graph = timed(g.replay)
     del g
 
+    full = decode_full_step(sq, torch, stream, layer_ws, head, nw, eps, xh, tokens)
+
     # The drop-in path as the Go binding would drive it: host buffers in and
     # out of every call (x uploaded, dst downloaded, synchronous), with the
     # host-side multi-weight and SwiGLU entries: 129 calls per token.
@@ -464,7 +466,7 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     ms_host = (time.time() - t0) / nh * 1e3
     del layer_ws, head
     torch.cuda.empty_cache()
-    return {"decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
+    return {**full, "decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
             "decode_gemv_tok_s_without_norms": round(1e3 / ms_plain, 1),
             "decode_gemv_tok_s_graph": round(1e3 / ms_graph, 1),
             "decode_gemv_ms_per_token_graph": round(ms_graph, 4),
@@ -479,6 +481,106 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
                            "prologues; decode_host_entry_"
                            "tok_s: the same 129 calls through the host-buffer entry points (x in, dst out, "
                            "synchronous, from Python); attention and norms not included"}
+
+
+def decode_full_step(sq, torch, stream, layer_ws, head, nw, eps, xh, tokens: int) -> dict:
+    """The whole decode step on the device at stated KV positions: per layer
+    RMSNorm + q/k/v, the attention section (bias / norm / RoPE / KV append /
+    causal GQA attention over the cache), o + residual add, RMSNorm + gate/up
+    + SwiGLU, down + residual add; then RMSNorm + head + greedy argmax
+    (forwardBlock model_f32.go:382-500, outputLogits :502-527). x starts from
+    the same embedding row every token (a device copy); the cache is set back
+    to `pos` rows before each token, so every timed token runs at position pos."""
+    import numpy as np
+    H, F, L, NH, NKV, DK = 4096, 14336, 32, 32, 8, 128
+    P = lambda t: t.data_ptr()
+    half = DK // 2
+    freqs = torch.from_numpy(np.array([1.0 / 500000.0 ** (2.0 * i / DK) for i in range(half)], np.float32)).cuda()
+    prm = sq.AttnParams(n_heads=NH, n_kv_heads=NKV, d_k=DK, rope_half_dim=half, rope_freqs=P(freqs), norm_eps=eps)
+    kvc = sq.KVCache(L, NKV, DK, 2048 + 16)
+    x = torch.empty(H, device="cuda")
+    q, k, v = (torch.empty(n, device="cuda") for n in (H, NKV * DK, NKV * DK))
+    att = torch.empty(H, device="cuda")
+    h = torch.empty(F, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    sp = stream.cuda_stream
+
+    def token(pos, sp):
+        kvc.set_length(pos)
+        x.copy_(xh)
+        for li, (wq, wk, wv, wo, wg, wu, wd) in enumerate(layer_ws):
+            sq.rmsnorm_matmul_multi_dev([wq, wk, wv], P(x), P(nw), eps, 1, H, [P(q), P(k), P(v)], sp)
+            sq.attention_dev(kvc, li, prm, P(q), P(k), P(v), 1, pos, P(att), sp)
+            sq.matmul_add_dev(wo, P(att), 1, H, P(x), sp)
+            sq.rmsnorm_matmul_swiglu_dev(wg, wu, P(x), P(nw), eps, 1, H, P(h), sp)
+            sq.matmul_add_dev(wd, P(h), 1, F, P(x), sp)
+        sq.rmsnorm_matmul_argmax_dev(head, P(x), P(nw), eps, P(tok), 0, sp)
+
+    def attention_only(pos, sp):
+        kvc.set_length(pos)
+        for li in range(L):
+            sq.attention_dev(kvc, li, prm, P(q), P(k), P(v), 1, pos, P(att), sp)
+
+    def timed(run, n, st) -> float:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(st)
+        for _ in range(n):
+            run()
+        b.record(st)
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    def graph_of(fn, pos, cs):
+        # eager uses on cs first: its workspace, counters and argmax scratch
+        # are allocated before the capture
+        with torch.cuda.stream(cs):
+            fn(pos, cs.cuda_stream)
+            fn(pos, cs.cuda_stream)
+        cs.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cs):
+            fn(pos, cs.cuda_stream)
+        return g
+
+    res = {}
+    cs = torch.cuda.Stream()
+    for pos in (128, 2047):
+        # eager, driven from Python (host-bound: five ctypes calls per layer)
+        for _ in range(2):
+            token(pos, stream.cuda_stream)
+        torch.cuda.synchronize()
+        ms_eager = timed(lambda: token(pos, stream.cuda_stream), tokens, stream)
+        want = int(tok.item())
+        # the same launches replayed from a HIP graph: the GPU-side cost
+        g = graph_of(token, pos, cs)
+        tok.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        same = int(tok.item()) == want
+        ms = timed(g.replay, tokens, stream)  # replay() runs on the current stream
+        del g
+        ga = graph_of(attention_only, pos, cs)
+        ms_att = timed(ga.replay, max(tokens, 20), stream)
+        del ga
+        att_us = ms_att * 1e3 / L
+        kv_bytes = 2 * NKV * (pos + 1) * DK * 4  # K and V rows read per layer
+        res[f"decode_full_tok_s_kv{pos}"] = round(1e3 / ms, 1)
+        res[f"decode_full_ms_per_token_kv{pos}"] = round(ms, 4)
+        res[f"decode_full_eager_tok_s_kv{pos}"] = round(1e3 / ms_eager, 1)
+        res[f"decode_full_graph_matches_eager_kv{pos}"] = same
+        res[f"attention_us_per_layer_kv{pos}"] = round(att_us, 2)
+        res[f"attention_kv_GBps_kv{pos}"] = round(kv_bytes / (att_us * 1e-6) / 1e9, 1)
+    res["decode_full_note"] = ("whole step on the device: 32 x [RMSNorm+qkv, attention (prep + split-K "
+                               "kernel), o + residual, RMSNorm+gate/up+SwiGLU, down + residual] + RMSNorm+head+"
+                               "argmax, + one embedding-row copy: 193 launches per token at KV position pos "
+                               "(Llama-3-8B shape: 32 q heads, 8 kv heads, d_k 128, RoPE base 500000), replayed "
+                               "from a HIP graph (the GPU-side cost); _eager: the same calls issued from Python "
+                               "(host-bound). attention_us_per_layer: the two attention launches of one layer "
+                               "(graph of the 32 layers' calls); attention_kv_GBps: K and V bytes read per layer "
+                               "over that time")
+    kvc.close()
+    return res
 
 
 def cpu_baseline(sq, synth, gate_raw, up_raw, down_raw, copies: int, step_bytes: int,

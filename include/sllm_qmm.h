@@ -256,7 +256,11 @@ typedef struct sllm_attn_params {
  * Scores are the reference's sequential float32 dots; the softmax sums and
  * the weighted sum of values are reassociated (split over the positions and
  * combined), and the per-head RMSNorm sums its squares in the library's
- * fixed order. Two launches; asynchronous on `stream`.
+ * fixed order. One row (decode): two launches (the attention over splits of
+ * the cached positions, which also prepares the row, then the combine of the
+ * splits); several rows: three (the row preparation first). Asynchronous on
+ * `stream`; allocates nothing once the stream's workspace has grown to the
+ * call's size.
  */
 sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q_dev,
                                const float *k_dev, const float *v_dev, int seq_len, int start_pos,

@@ -85,43 +85,6 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
     return SLLM_OK;
 }
 
-// Attention split counters per (device, stream): zeroed when allocated, left
-// zeroed by every attention launch.
-struct Cnt {
-    unsigned int *p = nullptr;
-    size_t n = 0;
-};
-std::unordered_map<uint64_t, Cnt> g_attn_cnt;
-
-sllm_status attn_counters(hipStream_t stream, size_t n, unsigned int **out) {
-    int dev = 0;
-    SLLM_HIP(hipGetDevice(&dev));
-    const uint64_t key = ((uint64_t)(uintptr_t)stream << 8) ^ (uint64_t)dev;
-    std::lock_guard<std::mutex> lk(g_mu);
-    Cnt &c = g_attn_cnt[key];
-    if (c.n < n) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return set_error(SLLM_ERR_ARG, "attention: this call would allocate counters on a capturing stream; "
-                                           "make a call with as many rows on the stream before capturing it");
-        if (c.p) {
-            SLLM_HIP(hipStreamSynchronize(stream));
-            (void)hipFree(c.p);
-            c.p = nullptr;
-            c.n = 0;
-        }
-        const size_t want = n < 4096 ? 4096 : n;
-        if (hipMalloc(&c.p, want * sizeof(unsigned int)) != hipSuccess) {
-            c.p = nullptr;
-            return set_error(SLLM_ERR_OOM, "attention counter allocation failed");
-        }
-        c.n = want;
-        SLLM_HIP(hipMemsetAsync(c.p, 0, want * sizeof(unsigned int), stream));
-    }
-    *out = c.p;
-    return SLLM_OK;
-}
-
 // The GEMM activation workspace of `stream` on the current device, grown to at
 // least `need` bytes. Growing synchronizes the stream before freeing the old
 // buffer (work already queued on it may still read it).
@@ -441,6 +404,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemv_wg_per_cu") && value >= 1 && value <= 8) t.gemv_wg_per_cu = value;
     else if (!std::strcmp(name, "gemv_max_nb") && value >= 1 && value <= 8) t.gemv_max_nb = value;
     else if (!std::strcmp(name, "gemv_inflight_kb") && value >= 64) t.gemv_inflight_kb = value;
+    else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;
@@ -1025,8 +989,6 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     void *ws = nullptr;
     size_t cap = 0;
     if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
-    unsigned int *cnt = nullptr;
-    if ((st = attn_counters(s, (size_t)seq_len * kv->n_kv, &cnt)) != SLLM_OK) return st;
     AttnArgs a{};
     a.q = q;
     a.k = k;
@@ -1057,7 +1019,6 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     a.out = out;
     a.qrot = (float *)ws;
     a.part = (float *)((char *)ws + align256((size_t)seq_len * p->n_heads * kv->d_k * sizeof(float)));
-    a.cnt = cnt;
     a.splits = splits;
     a.tps = tps;
     if ((st = launch_attention(a, s)) != SLLM_OK) return st;

@@ -2,14 +2,18 @@
 // model_f32.go:398-466) on device buffers: bias adds, per-head QK RMSNorm,
 // RoPE, the KV-cache append and the causal GQA attention with merged heads.
 //
-// attn_prep_kernel: one wave per (row, head) - bias, norm and RoPE of a q
-//   head into the workspace, of a kv head into the cache (v: bias only).
-// attn_kernel: one workgroup per (split, row, kv head). A split is a range
-//   of cached positions in tiles of 64 (one per lane); the workgroup stages a
-//   tile's K rows in LDS once for all q heads of the group (GQA: the kv head
-//   is read from HBM once), each wave owns one or two q heads. Scores are the
-//   reference's sequential float32 dots; the softmax runs online over the
-//   tiles; the last workgroup of a (row, kv head) combines the splits.
+// attn_split_kernel: one workgroup per (split, row, kv head). A split is a
+//   range of cached positions in tiles of 64 (one per lane); the workgroup
+//   stages a tile's K and V rows in LDS once for all q heads of the group
+//   (GQA: the kv head is read from HBM once), each wave owns one q head,
+//   and the split's partial softmax state goes to the workspace.
+//   Scores are the reference's sequential float32 dots. For one query row
+//   (decode) it also does the bias / norm / RoPE / append work itself.
+// attn_prep_kernel (several rows): that work, one wave per (row, head).
+// attn_combine_kernel: one wave per (row, head) merges the splits. Separate
+//   launches instead of a last-workgroup combine: on this multi-XCD part a
+//   device-scope fence writes back and invalidates the L2, which costs more
+//   than the launch.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -24,7 +28,10 @@ namespace {
 constexpr int kTile = 64;     // positions per tile: one per lane
 constexpr int kChunk = 128;   // K columns staged per pass (LDS: 64 x 132 floats)
 constexpr int kMaxDk = 256;   // head size limit (o: 4 values per lane)
-constexpr int kTargetBlocks = 512;
+
+// Native 4-float vector: arrays of it stay in registers (HIP's float4, a
+// union type, can keep a register array in scratch memory).
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float lane_bcast(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -33,26 +40,23 @@ __device__ __forceinline__ float lane_bcast(float v, int lane) {
 // Bias (model_f32.go:398-420), per-head RMSNorm (:424-435; rmsNormFlatF32,
 // float32_ops.go:159-172, the sum of squares in the library's association:
 // slot s < 256 adds x[s]^2, x[s+256]^2, ..., the four groups of 64 slots are
-// wave sums added left to right), RoPE (applyRopeInPlaceF32, float32_ops.go:
-// 174-188) and the cache append (:445-448).
-__global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
-    __shared__ float row[kMaxDk];
-    const int s = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-    const bool isq = t < a.n_heads;
-    const int h = isq ? t : t - a.n_heads;
-    const int dk = a.d_k;
-    const int cols = (isq ? a.n_heads : a.n_kv) * dk;
-    const float *src = (isq ? a.q : a.k) + (size_t)s * cols + (size_t)h * dk;
-    const float *bias = isq ? a.q_bias : a.k_bias;
-    const int blen = isq ? a.qb_len : a.kb_len;
-    const float *nw = isq ? a.q_norm : a.k_norm;
+// wave sums added left to right) and RoPE (applyRopeInPlaceF32,
+// float32_ops.go:174-188) of one head row, by one wave, into row (LDS).
+// j0: the row's offset in the full q / k row (the bias index).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+__device__ void prep_row(float *row, const float *src, int dk, const float *bias, int j0, int blen,
+                         const float *nw, float eps, const float *freqs, int half, int pos, int lane) {
+    // this lane's first rotation frequency, loaded with the row (half <= 64 in one pass)
+    const float f0 = lane < half ? freqs[lane] : 0.0f;
     for (int d = lane; d < dk; d += 64) {
         float x = src[d];
-        const int j = h * dk + d;
-        if (bias && j < blen) x = x + bias[j];
+        if (bias && j0 + d < blen) x = x + bias[j0 + d];
         row[d] = x;
     }
-    __syncthreads();
+    wave_lds_sync();
     if (nw) {
         float w[4];
 #pragma unroll
@@ -62,14 +66,13 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
             w[q4] = wave_sum(p);
         }
         const float ss = ((w[0] + w[1]) + w[2]) + w[3];
-        const float inv = 1.0f / (float)sqrt((double)ss / (double)dk + (double)a.eps);
-        __syncthreads();
+        const float inv = 1.0f / (float)sqrt((double)ss / (double)dk + (double)eps);
+        wave_lds_sync();
         for (int d = lane; d < dk; d += 64) row[d] = (row[d] * inv) * nw[d];
-        __syncthreads();
+        wave_lds_sync();
     }
-    const int pos = a.start_pos + s;
-    for (int i = lane; i < a.half_dim; i += 64) {
-        const float ang = a.freqs[i] * (float)pos;
+    for (int i = lane; i < half; i += 64) {
+        const float ang = (i == lane ? f0 : freqs[i]) * (float)pos;
         double sd, cd;
         sincos((double)ang, &sd, &cd);
         const float c = (float)cd, sn = (float)sd;
@@ -77,7 +80,22 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
         row[2 * i] = x0 * c - x1 * sn;
         row[2 * i + 1] = x0 * sn + x1 * c;
     }
-    __syncthreads();
+    wave_lds_sync();
+}
+
+// Several rows (prefill): one wave per (row, head) - q heads into the
+// workspace, kv heads into the cache (k: bias, norm, RoPE; v: bias) at
+// rows cache_len + s (the append, model_f32.go:445-448).
+__global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
+    __shared__ float row[kMaxDk];
+    const int s = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const bool isq = t < a.n_heads;
+    const int h = isq ? t : t - a.n_heads;
+    const int dk = a.d_k;
+    const int cols = (isq ? a.n_heads : a.n_kv) * dk;
+    prep_row(row, (isq ? a.q : a.k) + (size_t)s * cols + (size_t)h * dk, dk, isq ? a.q_bias : a.k_bias, h * dk,
+             isq ? a.qb_len : a.kb_len, isq ? a.q_norm : a.k_norm, a.eps, a.freqs, a.half_dim, a.start_pos + s,
+             lane);
     if (isq) {
         float *dst = a.qrot + ((size_t)s * a.n_heads + h) * dk;
         for (int d = lane; d < dk; d += 64) dst[d] = row[d];
@@ -87,8 +105,7 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
         for (int d = lane; d < dk; d += 64) {
             a.cache_k[at + d] = row[d];
             float x = vs[d];
-            const int j = h * dk + d;
-            if (a.v_bias && j < a.vb_len) x = x + a.v_bias[j];
+            if (a.v_bias && h * dk + d < a.vb_len) x = x + a.v_bias[h * dk + d];
             a.cache_v[at + d] = x;
         }
     }
@@ -97,142 +114,259 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
 // fusedAttentionHeadF32 (float32_ops.go:190-235) for the q heads of one kv
 // head (repeatKVDataF32, float32_ops.go:252-260: q head g*rep + r reads kv
 // head g) and one query row, over one split of the positions the causal mask
-// leaves (0 .. cache_len + qi). Score = (sequential float32 dot) * scale, as
-// the reference computes it; the exponentials are float32(exp(float64(score
-// - running max))), rescaled by the same form when the running max grows, and
-// the splits are combined with weights float32(exp(float64(m_split - max))).
-// Against the reference's single pass (exps relative to the global max, one
-// sequential sum, terms (e * invSum) * v) only the association of the sums
-// and these rescalings differ.
-__global__ void __launch_bounds__(256) attn_kernel(AttnArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float kt[];  // kTile x (kChunk + 4)
-    __shared__ int last;
+// leaves (0 .. cache_len + qi): writes the split's running max, sum of
+// exponentials and exponential-weighted sum of values per head. Score =
+// (sequential float32 dot) * scale, as the reference computes it; the
+// exponentials are float32(exp(float64(score - running max))), rescaled by
+// the same form when the running max grows.
+//
+// Wave r owns q head r of the group (max(4, rep) waves); lane l holds the
+// values d = l + 64 j, j < DKL (DKL = d_k / 64 rounded up). PREP (one query
+// row): the waves first build their q heads (bias, norm, RoPE) in LDS, and
+// the workgroup whose range holds the new position builds the new k / v row,
+// appends it to the cache and uses it from LDS; otherwise attn_prep_kernel
+// has done both. Per tile the K and V rows are loaded together (K straight
+// to LDS, V to registers while the scores are computed, then to the same LDS
+// buffer): one memory latency per tile, overlapped with the q preparation
+// for the first. LDS reads are issued in groups of eight.
+template <bool PREP, int DKL>
+__global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
+
+    extern __shared__ __attribute__((aligned(16))) float lds[];
     constexpr int ks = kChunk + 4;
+    float *kt = lds;                   // kTile x ks: a K chunk, then a V chunk
+    float *qs = lds + kTile * ks;      // rep x d_k: the group's rotated q heads
+    float *nk = qs + a.rep * a.d_k;    // PREP: the new k and v rows (2 x d_k)
+    const int nt = blockDim.x;
     const int split = blockIdx.x;
     const int qi = blockIdx.y / a.n_kv, g = blockIdx.y - qi * a.n_kv;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int r = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's q head in the group
+    const bool head = r < a.rep;
     const int dk = a.d_k;
     const int limit = a.cache_len + qi + 1;
     const int p0 = split * a.tps * kTile;
     const int p1 = min(p0 + a.tps * kTile, limit);
+    // rows read from the cache: PREP builds the new one (position cache_len) itself
+    const int have = PREP ? a.cache_len : limit;
+    const bool owns_new = PREP && a.cache_len >= p0 && a.cache_len < p1;
     const float *kb = a.cache_k + (size_t)g * a.cap * dk;
     const float *vb = a.cache_v + (size_t)g * a.cap * dk;
-    const float *qg = a.qrot + ((size_t)qi * a.n_heads + (size_t)g * a.rep) * dk;
+    constexpr bool one_chunk = DKL <= 2;  // d_k <= kChunk
 
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
-    float o[2][4] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
-    for (int t0 = p0; t0 < p1; t0 += kTile) {
-        const int n = min(kTile, p1 - t0);  // valid positions of this tile (lanes < n)
-        float dot[2] = {0.0f, 0.0f};
-        for (int c0 = 0; c0 < dk; c0 += kChunk) {
-            const int cw = min(kChunk, dk - c0);
-            const int q4 = cw / 4;
-            __syncthreads();  // the previous chunk's readers are done
-            for (int i = threadIdx.x; i < n * q4; i += 256) {
-                const int p = i / q4, c = (i - p * q4) * 4;
-                *(float4 *)(kt + p * ks + c) = *(const float4 *)(kb + (size_t)(t0 + p) * dk + c0 + c);
-            }
-            __syncthreads();
+    v4f kreg[8], vreg[8];
+    auto load_chunk = [&](int t0, int n, int c0, bool k_too, bool v_too) {
+        const int q4 = min(kChunk, dk - c0) / 4;
 #pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int r = wave + 4 * j;
-                if (r >= a.rep || lane >= n) continue;
-                const float *qr = qg + (size_t)r * dk + c0;
-                const float *kr = kt + lane * ks;
-                float acc = dot[j];
-                for (int d = 0; d < cw; d += 4) {
-                    const float4 k4 = *(const float4 *)(kr + d);
-                    const float4 q = *(const float4 *)(qr + d);
-                    acc += q.x * k4.x;
-                    acc += q.y * k4.y;
-                    acc += q.z * k4.z;
-                    acc += q.w * k4.w;
+        for (int u = 0; u < 8; u++) {
+            const int i = tid + nt * u;
+            if (i < n * q4) {
+                const int p = i / q4, c = (i - p * q4) * 4;
+                if (t0 + p < have) {
+                    const size_t at = (size_t)(t0 + p) * dk + c0 + c;
+                    if (k_too) kreg[u] = *(const v4f *)(kb + at);
+                    if (v_too) vreg[u] = *(const v4f *)(vb + at);
                 }
-                dot[j] = acc;
             }
         }
+    };
+    auto store_chunk = [&](const v4f *reg, int n, int c0, int newp, const float *newrow) {
+        const int q4 = min(kChunk, dk - c0) / 4;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int r = wave + 4 * j;
-            if (r >= a.rep) continue;  // wave-uniform
-            const float s = lane < n ? dot[j] * a.scale : -INFINITY;
-            float mt = s;
+        for (int u = 0; u < 8; u++) {
+            const int i = tid + nt * u;
+            if (i < n * q4) {
+                const int p = i / q4, c = (i - p * q4) * 4;
+                *(v4f *)(kt + p * ks + c) = (p == newp) ? *(const v4f *)(newrow + c0 + c) : reg[u];
+            }
+        }
+    };
+    // the first tile's K (and V) rows: issued before anything waits
+    if (p0 < p1) load_chunk(p0, min(kTile, p1 - p0), 0, true, one_chunk);
+
+    if (PREP) {
+        const int pos = a.start_pos + qi;
+        if (head) {
+            const int h = g * a.rep + r;
+            prep_row(qs + r * dk, a.q + (size_t)qi * a.n_heads * dk + (size_t)h * dk, dk, a.q_bias, h * dk, a.qb_len,
+                     a.q_norm, a.eps, a.freqs, a.half_dim, pos, lane);
+        }
+        if (owns_new && r == (nt >> 6) - 1) {  // the last wave: no q head unless rep fills the workgroup
+            const size_t off = (size_t)qi * a.n_kv * dk + (size_t)g * dk;
+            prep_row(nk, a.k + off, dk, a.k_bias, g * dk, a.kb_len, a.k_norm, a.eps, a.freqs, a.half_dim, pos, lane);
+            const size_t at = ((size_t)g * a.cap + (size_t)a.cache_len) * dk;
+            for (int d = lane; d < dk; d += 64) {
+                float x = a.v[off + d];
+                if (a.v_bias && g * dk + d < a.vb_len) x = x + a.v_bias[g * dk + d];
+                nk[dk + d] = x;
+                a.cache_k[at + d] = nk[d];
+                a.cache_v[at + d] = x;
+            }
+        }
+    } else {
+        const float4 *qg = (const float4 *)(a.qrot + ((size_t)qi * a.n_heads + (size_t)g * a.rep) * dk);
+        for (int i = tid; i < a.rep * dk / 4; i += nt) ((float4 *)qs)[i] = qg[i];
+    }
+
+    float m = -INFINITY, l = 0.0f, o[DKL];
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
-            const float mn = fmaxf(m[j], mt);
-            const float alpha = (float)exp((double)(m[j] - mn));
-            const float e = lane < n ? (float)exp((double)(s - mn)) : 0.0f;
-            l[j] = l[j] * alpha + wave_sum(e);
+    for (int j = 0; j < DKL; j++) o[j] = 0.0f;
+    for (int t0 = p0; t0 < p1; t0 += kTile) {
+        const int n = min(kTile, p1 - t0);  // valid positions of this tile (lanes < n)
+        const int newp = owns_new ? a.cache_len - t0 : -1;  // row of the new position in this tile
+        float dot = 0.0f;
+        for (int c0 = 0; c0 < dk; c0 += kChunk) {
+            const int cw = min(kChunk, dk - c0);
+            if (t0 != p0 || c0 != 0) load_chunk(t0, n, c0, true, one_chunk);
+            __syncthreads();  // the previous users of kt are done (and qs / nk are written)
+            store_chunk(kreg, n, c0, newp, nk);
+            __syncthreads();
+            if (head && lane < n) {
+                const float *qr = qs + r * dk + c0;
+                const float *kr = kt + lane * ks;
+                for (int d0 = 0; d0 < cw; d0 += 32) {
+                    // eight 4-element steps: their LDS reads issue together, the
+                    // products are added one by one in element order
+                    v4f kv[8], qv[8];
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) o[j][jj] = o[j][jj] * alpha;
-#pragma unroll 4
-            for (int p = 0; p < n; p++) {
-                const float ep = lane_bcast(e, p);
-                const float *vr = vb + (size_t)(t0 + p) * dk;
+                    for (int u = 0; u < 8; u++) {
+                        kv[u] = *(const v4f *)(kr + d0 + 4 * u);
+                        qv[u] = *(const v4f *)(qr + d0 + 4 * u);
+                    }
+                    const int steps = min(8, (cw - d0) / 4);
 #pragma unroll
-                for (int jj = 0; jj < 4; jj++) {
-                    const int d = lane + 64 * jj;
-                    if (d < dk) o[j][jj] = o[j][jj] + ep * vr[d];
+                    for (int u = 0; u < 8; u++) {
+                        if (u < steps) {
+                            dot += qv[u].x * kv[u].x;
+                            dot += qv[u].y * kv[u].y;
+                            dot += qv[u].z * kv[u].z;
+                            dot += qv[u].w * kv[u].w;
+                        }
+                    }
                 }
             }
-            m[j] = mn;
+        }
+        // online softmax of this tile
+        float e = 0.0f;
+        if (head) {
+            const float sc = lane < n ? dot * a.scale : -INFINITY;
+            float mt = sc;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+            const float mn = fmaxf(m, mt);
+            const float alpha = (float)exp((double)(m - mn));
+            e = lane < n ? (float)exp((double)(sc - mn)) : 0.0f;
+            l = l * alpha + wave_sum(e);
+            m = mn;
+#pragma unroll
+            for (int j = 0; j < DKL; j++) o[j] = o[j] * alpha;
+        }
+        // o += sum over the tile's positions of e_p * V[p], V chunk by chunk in LDS
+        for (int c0 = 0; c0 < dk; c0 += kChunk) {
+            const int cw = min(kChunk, dk - c0);
+            if (!one_chunk) load_chunk(t0, n, c0, false, true);
+            __syncthreads();  // the score readers of kt are done
+            store_chunk(vreg, n, c0, newp, nk + dk);
+            __syncthreads();
+            if (head) {
+                for (int q0 = 0; q0 < n; q0 += 8) {
+                    // eight positions' values read together, then added in order
+                    float vv[8][DKL];
+#pragma unroll
+                    for (int pp = 0; pp < 8; pp++) {
+                        const float *vr = kt + (q0 + pp) * ks - c0;
+#pragma unroll
+                        for (int j = 0; j < DKL; j++) {
+                            const int d = lane + 64 * j;
+                            // rows past the tile's end hold stale LDS data: zero, not
+                            // a zero weight times whatever is there (NaN * 0 is NaN)
+                            vv[pp][j] = (q0 + pp < n && d >= c0 && d < c0 + cw) ? vr[d] : 0.0f;
+                        }
+                    }
+#pragma unroll
+                    for (int pp = 0; pp < 8; pp++) {
+                        const float ep = lane_bcast(e, q0 + pp);  // 0 past the tile's end
+#pragma unroll
+                        for (int j = 0; j < DKL; j++) {
+                            const int d = lane + 64 * j;
+                            if (d >= c0 && d < c0 + cw) o[j] = o[j] + ep * vv[pp][j];
+                        }
+                    }
+                }
+            }
         }
     }
 
-    // this split's partial of each head: running max, sum, weighted values
-    const size_t stride = (size_t)dk + 2;
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int r = wave + 4 * j;
-        if (r >= a.rep) continue;
+    // this split's partial of the head: running max, sum, weighted values
+    if (head) {
+        const size_t stride = (size_t)dk + 2;
         const int h = g * a.rep + r;
         float *pp = a.part + (((size_t)qi * a.n_heads + h) * a.splits + split) * stride;
         if (lane == 0) {
-            pp[0] = m[j];
-            pp[1] = l[j];
+            pp[0] = m;
+            pp[1] = l;
         }
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const int d = lane + 64 * jj;
-            if (d < dk) pp[2 + d] = o[j][jj];
+        for (int j = 0; j < DKL; j++) {
+            const int d = lane + 64 * j;
+            if (d < dk) pp[2 + d] = o[j];
         }
     }
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(&a.cnt[blockIdx.y], 1u) == (unsigned int)(a.splits - 1);
-    __syncthreads();
-    if (!last) return;
-    // the last workgroup of this (row, kv head): every other split's partials
-    // were written before its count (fence, then count)
-    __threadfence();
+}
+
+// The splits of one (row, head), one wave each: M = max of the split maxima,
+// weights w_t = float32(exp(float64(m_t - M))), L = sum of l_t * w_t (fixed
+// lane order), out[d] = (sum over t of o_t[d] * w_t) * (1 / L), written in
+// mergeHeadsDataF32's layout (float32_ops.go:262-273).
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);  // qi * n_heads + h
+    if (pair >= a.seq * a.n_heads) return;                 // wave-uniform
+    const int dk = a.d_k;
+    const size_t stride = (size_t)dk + 2;
+    const float *pb = a.part + (size_t)pair * a.splits * stride;
+    // splits in groups of 16: lane t holds m_t and l_t of its group, every
+    // lane the values of its d for the whole group - all loaded together
+    // (a group's missing splits weigh 0 and add exact zeros)
+    float M = -INFINITY;
+    for (int t = lane; t < a.splits; t += 64) M = fmaxf(M, pb[t * stride]);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const int r = wave + 4 * j;
-        if (r >= a.rep) continue;
-        const int h = g * a.rep + r;
-        const float *pb = a.part + ((size_t)qi * a.n_heads + h) * a.splits * stride;
-        float M = -INFINITY;
-        for (int t = 0; t < a.splits; t++) M = fmaxf(M, pb[t * stride]);
-        float L = 0.0f, O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int t = 0; t < a.splits; t++) {
-            const float w = (float)exp((double)(pb[t * stride] - M));
-            L = L + pb[t * stride + 1] * w;
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float Lp = 0.0f;
+    float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int t0 = 0; t0 < a.splits; t0 += 16) {
+        const int nt = min(16, a.splits - t0);
+        const int tl = t0 + (lane & 15);
+        const bool mine = lane < 16 && tl < a.splits;
+        const float ml = mine ? pb[tl * stride] : -INFINITY;
+        const float ll = mine ? pb[tl * stride + 1] : 0.0f;
+        float ov[16][4];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const float *ob = pb + (size_t)(t0 + u) * stride + 2;
 #pragma unroll
             for (int jj = 0; jj < 4; jj++) {
                 const int d = lane + 64 * jj;
-                if (d < dk) O[jj] = O[jj] + pb[t * stride + 2 + d] * w;
+                ov[u][jj] = (u < nt && d < dk) ? ob[d] : 0.0f;
             }
         }
-        const float inv = 1.0f / L;
-        float *dst = a.out + ((size_t)qi * a.n_heads + h) * dk;  // mergeHeadsDataF32 layout
+        const float wl = mine ? (float)exp((double)(ml - M)) : 0.0f;
+        Lp = Lp + ll * wl;
 #pragma unroll
-        for (int jj = 0; jj < 4; jj++) {
-            const int d = lane + 64 * jj;
-            if (d < dk) dst[d] = O[jj] * inv;
+        for (int u = 0; u < 16; u++) {
+            const float w = lane_bcast(wl, u);  // 0 past the group's end
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) O[jj] = O[jj] + ov[u][jj] * w;
         }
     }
-    if (threadIdx.x == 0) __hip_atomic_store(&a.cnt[blockIdx.y], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float L = wave_sum(Lp);
+    const float inv = 1.0f / L;
+    float *dst = a.out + (size_t)pair * dk;  // mergeHeadsDataF32 layout
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        const int d = lane + 64 * jj;
+        if (d < dk) dst[d] = O[jj] * inv;
+    }
 }
 
 }  // namespace
@@ -241,7 +375,8 @@ void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *sp
                     size_t *ws_bytes) {
     const int tiles = (kv_len + kTile - 1) / kTile;
     const int pairs = seq * n_kv;
-    int S = (kTargetBlocks + pairs - 1) / pairs;
+    const int target = tuning().attn_target_blocks;
+    int S = (target + pairs - 1) / pairs;
     S = S < 1 ? 1 : (S > tiles ? tiles : S);
     const int t = (tiles + S - 1) / S;
     S = (tiles + t - 1) / t;
@@ -252,11 +387,28 @@ void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *sp
     *ws_bytes = ((qrot + 255) & ~(size_t)255) + part;
 }
 
+template <bool PREP>
+void launch_split(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t s) {
+    const dim3 block(64 * (a.rep > 4 ? a.rep : 4));
+    switch ((a.d_k + 63) / 64) {
+    case 1: hipLaunchKernelGGL((attn_split_kernel<PREP, 1>), grid, block, lds, s, a); break;
+    case 2: hipLaunchKernelGGL((attn_split_kernel<PREP, 2>), grid, block, lds, s, a); break;
+    case 3: hipLaunchKernelGGL((attn_split_kernel<PREP, 3>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<PREP, 4>), grid, block, lds, s, a); break;
+    }
+}
+
 sllm_status launch_attention(const AttnArgs &a, hipStream_t s) {
-    hipLaunchKernelGGL(attn_prep_kernel, dim3(a.seq, a.n_heads + a.n_kv), dim3(64), 0, s, a);
+    const size_t lds = ((size_t)kTile * (kChunk + 4) + (size_t)(a.rep + 2) * a.d_k) * sizeof(float);
+    if (a.seq == 1) {
+        launch_split<true>(a, dim3(a.splits, a.n_kv), lds, s);
+    } else {
+        hipLaunchKernelGGL(attn_prep_kernel, dim3(a.seq, a.n_heads + a.n_kv), dim3(64), 0, s, a);
+        SLLM_HIP(hipGetLastError());
+        launch_split<false>(a, dim3(a.splits, a.seq * a.n_kv), lds, s);
+    }
     SLLM_HIP(hipGetLastError());
-    const size_t lds = (size_t)kTile * (kChunk + 4) * sizeof(float);
-    hipLaunchKernelGGL(attn_kernel, dim3(a.splits, a.seq * a.n_kv), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(attn_combine_kernel, dim3((a.seq * a.n_heads + 3) / 4), dim3(256), 0, s, a);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

@@ -156,7 +156,6 @@ struct AttnArgs {
     float *out;                // seq x n_heads*d_k (merged heads)
     float *qrot;               // workspace: seq x n_heads x d_k
     float *part;               // workspace: seq x n_heads x splits x (d_k + 2)
-    unsigned int *cnt;         // seq x n_kv counters, zero before and after each launch
     int splits, tps;           // splits per (row, kv head); tiles of 64 positions per split
 };
 // Split plan and workspace bytes (qrot + partials) of an attention call.
@@ -171,6 +170,7 @@ struct Tuning {
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
+    int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
 };
 Tuning &tuning();
 

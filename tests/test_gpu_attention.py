@@ -152,6 +152,22 @@ def test_decode_llama_heads(cache_len):
     run_case(m, 1, cache_len, rng)
 
 
+def test_first_position_after_a_launch_that_leaves_nan_in_lds():
+    # a tile with one row: the value loop must not multiply stale LDS rows
+    # (here NaN activations a GEMV staged there) by zero weights
+    K, N = 4096, 14336
+    raw = make_raw("q8", N, K, seed=3)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight("q8", raw, K // 32, N, K))
+    xn = torch.full((K,), float("nan"), device="cuda")
+    y = torch.empty(N, device="cuda")
+    sq.matmul_dev(w, xn.data_ptr(), 1, K, y.data_ptr())
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(99)
+    m = Model(8, 2, 128, 64, rng)
+    got, _ = run_case(m, 1, 0, rng)
+    assert np.all(np.isfinite(got))
+
+
 @pytest.mark.parametrize("seq,cache_len", [(37, 0), (5, 70), (70, 3)])
 def test_prefill_rows_are_causal(seq, cache_len):
     rng = np.random.default_rng(seq * 7 + cache_len)
