@@ -232,7 +232,11 @@ def config_table(sq, synth, torch, stream) -> dict:
     def copies(make_one):
         w0 = make_one()
         n = int(min(512, max(2, -(-ROTATE_BYTES // w0.plane_bytes))))
-        q = sq.QuantWeight(w0.qtype, w0.export(), w0.groups, w0.rows, w0.cols)
+        raw = w0.export()
+        if w0.qtype in ("q2k", "q3k"):  # native k-quants: rebuilt from their GGUF blocks
+            t = {"q2k": synth.GGML_Q2_K, "q3k": synth.GGML_Q3_K}[w0.qtype]
+            return [w0] + [sq.load_weight_f32_direct(t, raw, w0.rows, w0.cols) for _ in range(n - 1)]
+        q = sq.QuantWeight(w0.qtype, raw, w0.groups, w0.rows, w0.cols)
         return [w0] + [sq.DeviceWeight.from_quant(q) for _ in range(n - 1)]
 
     def run(ws, M, reps):
@@ -286,6 +290,16 @@ def config_table(sq, synth, torch, stream) -> dict:
     for M in (64, 512):
         table[f"C3 q8 down {H}x{F} M={M}"] = run(d, M, 20)
     del d
+    # native Q2_K / Q3_K (the reference's dense-fp32 types): GEMV over the
+    # native blocks; dense_fp32_equiv_GBps counts the 4 B / weight the
+    # reference's dense layout would stream in the same time
+    for t, name, make in ((synth.GGML_Q2_K, "q2k", synth.q2k_blocks), (synth.GGML_Q3_K, "q3k", synth.q3k_blocks)):
+        for N, K in ((F, H), (H, F)):
+            ws = copies(lambda: sq.load_weight_f32_direct(t, make(40 + t, N, K), N, K))
+            r = run(ws, 1, 200)
+            r["dense_fp32_equiv_GBps"] = round(4.0 * N * K / (r["us"] * 1e-6) / 1e9, 1)
+            table[f"{name} native {N}x{K} M=1"] = r
+            del ws
     torch.cuda.empty_cache()
     return table
 

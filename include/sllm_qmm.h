@@ -42,7 +42,9 @@ typedef enum {
     SLLM_Q4_0 = 1,  /* "q4"   18 B / 32: f16 d, 16 nibble bytes, w = d*(nib-8)        */
     SLLM_Q4_1 = 2,  /* "q4_1" 20 B / 32: f16 d, f16 m, 16 nibble bytes, w = d*nib+m   */
     SLLM_Q5_0 = 3,  /* "q5"   22 B / 32: f16 d, u32 qh, 16 nibble bytes, w = d*(q5-16)*/
-    SLLM_Q5K1 = 4   /* "q5k1" Q5_K as two summed Q4_1 tensors (kquant_kernels.go:103-154) */
+    SLLM_Q5K1 = 4,  /* "q5k1" Q5_K as two summed Q4_1 tensors (kquant_kernels.go:103-154) */
+    SLLM_Q2K = 5,   /* GGUF Q2_K kept native (84 B / 256); the reference loads it as dense fp32 */
+    SLLM_Q3K = 6    /* GGUF Q3_K kept native (110 B / 256); the reference loads it as dense fp32 */
 } sllm_qtype;
 
 typedef struct sllm_weight sllm_weight;
@@ -81,7 +83,14 @@ sllm_status sllm_weight_from_quant(const char *qtype, const void *raw, size_t ra
  *   12 Q4_K -> Q4_1 (convertQ4KToQ41, kquant_kernels.go:30-63);
  *   13 Q5_K -> Q5K1 (convertQ5KToTwoQ41, kquant_kernels.go:110-154);
  *   14 Q6_K, 20 IQ4_NL -> Q8_0 (dequantize in fp64 + quantizeQ8Rows,
- *      gguf.go:889-894,912-921,979-1015,1080-1134).
+ *      gguf.go:889-894,912-921,979-1015,1080-1134);
+ *   10 Q2_K, 11 Q3_K -> kept native (SLLM_Q2K / SLLM_Q3K). The reference
+ *      dequantizes these to dense fp32 (gguf.go:907-911, dequantizeQ2KNative /
+ *      dequantizeQ3KNative kquants.go:147-245) and multiplies with the plain
+ *      float32 loop (modelMatmulFloatIntoF32, float32_ops.go:462-482); the
+ *      matmuls here rebuild each of those float32 weights exactly from the
+ *      native blocks and multiply fp32 activations by them, so only the order
+ *      of the row sums differs (no int8 activation codes for these types).
  * Other types return SLLM_ERR_QTYPE (the reference's dense-fp32 branch).
  */
 sllm_status sllm_weight_from_gguf(uint32_t ggml_type, const void *raw, size_t raw_bytes,
@@ -103,6 +112,7 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
 /*
  * Rebuild the reference Raw bytes (QuantWeight.Raw layout) from the device
  * planes into host memory (cap >= raw_bytes). Bit-exact inverse of the repack.
+ * SLLM_Q2K / SLLM_Q3K: the GGUF super-block bytes the weight was made from.
  */
 sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap);
 

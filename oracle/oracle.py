@@ -55,7 +55,7 @@ def lib() -> C.CDLL:
         L.ref_quantize_act_q8.argtypes = [P, i32, P, P]
         L.ref_quantize_q8_rows_f32.argtypes = [P, i32, i32, P]
         L.ref_quantize_q8_rows_f64.argtypes = [P, i32, i32, P]
-        for n in ("q8_0", "q4_0", "q4_1", "q5_0", "q4_k", "q5_k", "q6_k", "iq4_nl"):
+        for n in ("q8_0", "q4_0", "q4_1", "q5_0", "q4_k", "q5_k", "q6_k", "iq4_nl", "q2_k", "q3_k"):
             getattr(L, "ref_dequant_" + n).argtypes = [P, i64, P]
         L.ref_convert_q4k_to_q41.argtypes = [P, i32, i32, P]
         L.ref_convert_q5k_to_two_q41.argtypes = [P, i32, i32, P]
@@ -82,6 +82,8 @@ def lib() -> C.CDLL:
         L.ref_rmsnorm.argtypes = [P, P, C.c_float, i32, i32, P]
         L.ref_rmsnorm_lib.argtypes = [P, P, C.c_float, i32, i32, P]
         L.ref_rope.argtypes = [P, i32, i32, i32, P, i32]
+        L.ref_matmul_dense.argtypes = [P, i32, i32, P, i32, P]
+        L.ref_dense_block_sums.argtypes = [P, i32, i32, P, i32, P]
         L.ref_attention_head.argtypes = [P, P, P, i32, i32, i32, i32, i32, P, i32]
         L.ref_attention_layer.argtypes = [P, P, P, i32, i32, i32, i32, P, i32, P, i32, P, i32, P, P,
                                           C.c_float, i32, P, i32, i32, P, P, i32, i32, P, P]
@@ -349,3 +351,28 @@ def attention_layer(q, k, v, n_heads, n_kv, d_k, cache_k, cache_v, cache_len, st
                               _p(fr), half_dim, start_pos, _p(ck), _p(cv), cap, cache_len, _p(out),
                               _p(qr) if return_q_rot else None)
     return (out, ck, cv, qr) if return_q_rot else (out, ck, cv)
+
+
+def dense_weights(ggml_type: int, raw: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """The dense float32 weights the reference builds for a type it has no
+    quantized kernel for (gguf.go:907-911: f64ToF32(dequantize1D(...)))."""
+    kind = {10: "q2_k", 11: "q3_k"}[ggml_type]
+    return dequant(kind, raw, rows * cols).astype(np.float32).reshape(rows, cols)
+
+
+def matmul_dense(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """modelMatmulFloatIntoF32 (float32_ops.go:462-482): x (M x K) -> M x N."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, w.shape[1])
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    lib().ref_matmul_dense(_p(w), w.shape[0], w.shape[1], _p(x), x.shape[0], _p(out))
+    return out
+
+
+def dense_block_sums(w: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """The dense products summed per 32-element block from zero: M x N x K/32."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, w.shape[1])
+    out = np.empty((x.shape[0], w.shape[0], w.shape[1] // 32), np.float32)
+    lib().ref_dense_block_sums(_p(w), w.shape[0], w.shape[1], _p(x), x.shape[0], _p(out))
+    return out

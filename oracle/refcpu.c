@@ -936,3 +936,88 @@ void ref_attention_layer(float *q, float *k, float *v, int seq_len, int n_heads,
     free(vh);
     free(att);
 }
+
+/* ---- native k-quants and the dense fp32 path ---------------------------- */
+
+/* kquants.go:147-180 dequantizeQ2KNative: per 16-element sub-block the scale
+ * byte gives dl = d * (sc & 15) and ml = dmin * (sc >> 4); w = dl * q - ml in
+ * fp64, q the 2-bit code at bit pair `shift` of the code bytes. */
+void ref_dequant_q2_k(const uint8_t *raw, int64_t n, double *out) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *base = raw + b * 84;
+        const uint8_t *scales = base, *qs = base + 16;
+        const double d = ref_f16_to_f64(rd16(base + 80)), dmin = ref_f16_to_f64(rd16(base + 82));
+        double *o = out + b * 256;
+        int is = 0, qo = 0;
+        for (int half = 0; half < 2; half++) {
+            for (int j = 0, shift = 0; j < 4; j++, shift += 2) {
+                for (int sub = 0; sub < 2; sub++) {
+                    const uint8_t sc = scales[is++];
+                    const double dl = d * (double)(sc & 0x0f), ml = dmin * (double)(sc >> 4);
+                    for (int l = 0; l < 16; l++) *o++ = dl * (double)((qs[qo + 16 * sub + l] >> shift) & 3) - ml;
+                }
+            }
+            qo += 32;
+        }
+    }
+}
+
+/* kquants.go:183-245 dequantizeQ3KNative: the 16 six-bit scales unpacked from
+ * their 12 bytes (low nibbles in bytes 0..7, high bit pairs in bytes 8..11),
+ * dl = d * (scale - 32); w = dl * (q - sub) with sub = 0 where the element's
+ * high-mask bit (bit m, m = 1, 2, 4, ... per sub-block pair) is set, else 4. */
+void ref_dequant_q3_k(const uint8_t *raw, int64_t n, double *out) {
+    for (int64_t b = 0; b < n / 256; b++) {
+        const uint8_t *base = raw + b * 110;
+        const uint8_t *hmask = base, *qs = base + 32, *scb = base + 96;
+        const double d = ref_f16_to_f64(rd16(base + 108));
+        int scales[16];
+        for (int i = 0; i < 4; i++) {
+            scales[i] = (scb[i] & 0x0f) | (((scb[8 + i] >> 0) & 3) << 4);
+            scales[4 + i] = (scb[4 + i] & 0x0f) | (((scb[8 + i] >> 2) & 3) << 4);
+            scales[8 + i] = (scb[i] >> 4) | (((scb[8 + i] >> 4) & 3) << 4);
+            scales[12 + i] = (scb[4 + i] >> 4) | (((scb[8 + i] >> 6) & 3) << 4);
+        }
+        double *o = out + b * 256;
+        int is = 0, qo = 0;
+        uint8_t m = 1;
+        for (int half = 0; half < 2; half++) {
+            for (int j = 0, shift = 0; j < 4; j++, shift += 2, m = (uint8_t)(m << 1)) {
+                for (int sub = 0; sub < 2; sub++) {
+                    const double dl = d * (double)(scales[is++] - 32);
+                    for (int l = 0; l < 16; l++) {
+                        const double s = (hmask[16 * sub + l] & m) ? 0.0 : 4.0;
+                        *o++ = dl * ((double)((qs[qo + 16 * sub + l] >> shift) & 3) - s);
+                    }
+                }
+            }
+            qo += 32;
+        }
+    }
+}
+
+/* modelMatmulFloatIntoF32 (float32_ops.go:462-482): dst[i][j] = sequential
+ * float32 sum over l of x[i][l] * w[j][l]. */
+void ref_matmul_dense(const float *w, int N, int K, const float *x, int M, float *dst) {
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++) {
+            float sum = 0.0f;
+            const float *xr = x + (size_t)i * K, *wr = w + (size_t)j * K;
+            for (int l = 0; l < K; l++) sum += xr[l] * wr[l];
+            dst[(size_t)i * N + j] = sum;
+        }
+}
+
+/* The same products summed per 32-element block, each from zero in element
+ * order: out[i][j][g] (float32). */
+void ref_dense_block_sums(const float *w, int N, int K, const float *x, int M, float *out) {
+    const int G = K / 32;
+    for (int i = 0; i < M; i++)
+        for (int j = 0; j < N; j++)
+            for (int g = 0; g < G; g++) {
+                float sum = 0.0f;
+                const float *xr = x + (size_t)i * K + 32 * g, *wr = w + (size_t)j * K + 32 * g;
+                for (int l = 0; l < 32; l++) sum += xr[l] * wr[l];
+                out[((size_t)i * N + j) * G + g] = sum;
+            }
+}

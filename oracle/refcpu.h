@@ -45,6 +45,12 @@ void ref_dequant_q4_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.g
 void ref_dequant_q5_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.go:104-145 */
 void ref_dequant_q6_k(const uint8_t *raw, int64_t n, double *out);  /* gguf.go:979-1015 */
 void ref_dequant_iq4_nl(const uint8_t *raw, int64_t n, double *out);/* kquants.go:7-27 */
+void ref_dequant_q2_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.go:147-180 */
+void ref_dequant_q3_k(const uint8_t *raw, int64_t n, double *out);  /* kquants.go:183-245 */
+/* float32_ops.go:462-482 modelMatmulFloatIntoF32 (dense float32 weights). */
+void ref_matmul_dense(const float *w, int N, int K, const float *x, int M, float *dst);
+/* Its products summed per 32-element block from zero, element order. */
+void ref_dense_block_sums(const float *w, int N, int K, const float *x, int M, float *out);
 
 /* ---- load-time remaps / requantization ---------------------------------- */
 void ref_scale_min_k4(int j, const uint8_t *q, uint8_t *sc, uint8_t *m); /* kquants.go:62-71 */

@@ -460,6 +460,8 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     case 13: fmt = SLLM_Q5K1; per = 176; blk = 256; break;
     case 14: fmt = SLLM_Q8_0; per = 210; blk = 256; break;
     case 20: fmt = SLLM_Q8_0; per = 18; break;
+    case 10: fmt = SLLM_Q2K; per = 84; blk = 256; break;
+    case 11: fmt = SLLM_Q3K; per = 110; blk = 256; break;
     default:
         return set_error(SLLM_ERR_QTYPE, "GGUF type " + std::to_string(t) +
                                              " has no int8 kernel (the reference loads it as dense fp32)");
@@ -515,19 +517,23 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
     if (groups) *groups = w->groups;
     if (rows) *rows = w->rows;
     if (cols) *cols = w->cols;
-    if (raw_bytes) *raw_bytes = (size_t)w->rows * w->groups * raw_block_bytes(w->fmt);
+    if (raw_bytes) *raw_bytes = raw_bytes_of(w->fmt, (int64_t)w->rows * w->groups);
     return SLLM_OK;
 }
 
 sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap) {
     if (!w || !raw) return set_error(SLLM_ERR_ARG, "null pointer");
     const int64_t nb = (int64_t)w->rows * w->groups;
-    const size_t need = (size_t)nb * raw_block_bytes(w->fmt);
+    const size_t need = raw_bytes_of(w->fmt, nb);
     if (cap < need) return set_error(SLLM_ERR_ARG, "export buffer too small");
     std::vector<unsigned char> img(w->bytes);
     SLLM_HIP(hipMemcpy(img.data(), w->base, w->bytes, hipMemcpyDeviceToHost));
     MutPlanes p;
     carve_planes(w->fmt, nb, img.data(), &p);
+    if (kq_native(w->fmt)) {
+        export_kq_native(w->fmt, p, nb, (uint8_t *)raw);
+        return SLLM_OK;
+    }
     unsigned char *o = (unsigned char *)raw;
     auto put16 = [](unsigned char *dst, uint16_t v) { dst[0] = (unsigned char)v; dst[1] = (unsigned char)(v >> 8); };
     for (int64_t b = 0; b < nb; b++) {

@@ -569,6 +569,7 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 }  // namespace
 
 bool gemm_supported(int fmt, int G) {
+    if (kq_native(fmt)) return false;  // the GEMV takes every row count
     return fmt == SLLM_Q5_0 ? G >= 1 : G % kKB == 0;
 }
 

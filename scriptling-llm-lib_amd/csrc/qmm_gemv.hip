@@ -29,6 +29,14 @@ extern template sllm_status launch_mt<SLLM_Q5K1, false>(int, int, int, const Seg
                                                           int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q5K1, true>(int, int, int, const SegTable &, const float *, int, int, int,
                                                           int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q2K, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                         int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q2K, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                        int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q3K, false>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                         int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q3K, true>(int, int, int, const SegTable &, const float *, int, int, int,
+                                                        int, int, int, size_t, hipStream_t);
 }  // namespace gemv
 
 using namespace gemv;
@@ -160,6 +168,8 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         case SLLM_Q4_1: st = SLLM_GEMV_FMT(SLLM_Q4_1); break;
         case SLLM_Q5_0: st = SLLM_GEMV_FMT(SLLM_Q5_0); break;
         case SLLM_Q5K1: st = SLLM_GEMV_FMT(SLLM_Q5K1); break;
+        case SLLM_Q2K: st = SLLM_GEMV_FMT(SLLM_Q2K); break;
+        case SLLM_Q3K: st = SLLM_GEMV_FMT(SLLM_Q3K); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");
         }
 #undef SLLM_GEMV_FMT
@@ -265,6 +275,18 @@ __global__ void block_dots_kernel(Planes P, const float *__restrict__ x, int N, 
             out[t] = __builtin_bit_cast(int32_t, sum);
             continue;
         }
+        if (kq_native(FMT)) {
+            // the GEMV's own block term (elements in order) from a zero start
+            BlockRegs b;
+            load_block<FMT>(P, (uint32_t)idx, b);
+            ActRegs xa;
+#pragma unroll
+            for (int k = 0; k < 8; k++) xa.xf[k] = v[k];
+            float sum = 0.0f, unused = 0.0f;
+            block_term<FMT>(b, xa, sum, unused);
+            out[t] = __builtin_bit_cast(int32_t, sum);
+            continue;
+        }
         int w[8];
         float s;
         int sm;
@@ -346,6 +368,8 @@ sllm_status launch_block_dots(int fmt, const Planes &P, const float *x, int N, i
     case SLLM_Q4_1: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q4_1>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;
     case SLLM_Q5_0: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q5_0>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;
     case SLLM_Q5K1: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q5K1>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;
+    case SLLM_Q2K: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q2K>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;
+    case SLLM_Q3K: hipLaunchKernelGGL(block_dots_kernel<SLLM_Q3K>, dim3(grid), dim3(256), 0, s, P, x, N, G, M, out); break;
     default: return set_error(SLLM_ERR_QTYPE, "block_dots: unknown format");
     }
     SLLM_HIP(hipGetLastError());

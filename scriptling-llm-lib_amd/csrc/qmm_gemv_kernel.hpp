@@ -40,6 +40,11 @@ __device__ __forceinline__ int4 ld_nt(const int4 *p) {
 }
 __device__ __forceinline__ uint16_t ld_nt(const uint16_t *p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ uint32_t ld_nt(const uint32_t *p) { return __builtin_nontemporal_load(p); }
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 ld_nt(const uint2 *p) {
+    const v2u t = __builtin_nontemporal_load((const v2u *)p);
+    return make_uint2(t.x, t.y);
+}
 
 // LDS image of the prologue for MT activation rows of G blocks.
 struct ActView {
@@ -47,17 +52,17 @@ struct ActView {
     int4 *xh;   // [MT][G] elements 16..31
     float *xs;  // [MT][G] activation scale
     int *sx;    // [MT][G] Σxq
-    float *xf;  // Q5_0: [MT][G][kXfStride] fp32 activations
+    float *xf;  // fp32-activation formats: [MT][G][kXfStride] fp32 activations
 };
 
 __host__ __device__ inline size_t act_lds_bytes(int fmt, int MT, int G) {
-    if (fmt == SLLM_Q5_0) return (size_t)MT * G * kXfStride * sizeof(float);
+    if (act_f32(fmt)) return (size_t)MT * G * kXfStride * sizeof(float);
     return (size_t)MT * G * (2 * sizeof(int4) + sizeof(float) + sizeof(int));
 }
 
 __device__ inline ActView carve_act(unsigned char *lds, int fmt, int MT, int G) {
     ActView v{};
-    if (fmt == SLLM_Q5_0) {
+    if (act_f32(fmt)) {
         v.xf = (float *)lds;
     } else {
         v.xl = (int4 *)lds;
@@ -69,11 +74,12 @@ __device__ inline ActView carve_act(unsigned char *lds, int fmt, int MT, int G) 
 }
 
 // Writes one lane's part (8/TPB float4 = 32/TPB elements) of activation block
-// blk into LDS: quantized codes + scale + Σq, or (Q5_0) the fp32 values.
+// blk into LDS: quantized codes + scale + Σq, or (fp32-activation formats)
+// the fp32 values.
 template <int FMT, int TPB>
 __device__ __forceinline__ void stage_part(const float4 *v, int blk, int sub, const ActView &A) {
     constexpr int NV = 8 / TPB;
-    if (FMT == SLLM_Q5_0) {
+    if (act_f32(FMT)) {
         float4 *d = (float4 *)(A.xf + (size_t)blk * kXfStride) + sub * NV;
 #pragma unroll
         for (int k = 0; k < NV; k++) d[k] = v[k];
@@ -102,6 +108,8 @@ struct BlockRegs {
     int4 q, q2;
     uint16_t d, m, dh;
     uint32_t qh;
+    uint2 c2;      // native k-quants: the 2-bit codes
+    uint32_t sbw;  // native k-quants: the super-block's scale word
 };
 
 template <class T>
@@ -112,6 +120,13 @@ __device__ __forceinline__ const T *at(const T *base, uint32_t idx) {
 
 template <int FMT>
 __device__ __forceinline__ void load_block(const Planes &P, uint32_t idx, BlockRegs &b) {
+    if (kq_native(FMT)) {
+        b.c2 = ld_nt(at(P.q2, idx));
+        b.d = ld_nt(at(P.d, idx));
+        b.sbw = ld_nt(at(P.sb, idx >> 3));  // rows hold whole super-blocks (G % 8 == 0)
+        if (FMT == SLLM_Q3K) b.qh = ld_nt(at(P.qh, idx));
+        return;
+    }
     b.q = ld_nt(at(P.qs, idx));
     b.d = ld_nt(at(P.d, idx));
     if (FMT == SLLM_Q8_0) b.q2 = ld_nt(at(P.qs2, idx));
@@ -137,7 +152,7 @@ struct ActRegs {
 
 template <int FMT>
 __device__ __forceinline__ void load_act(const ActView &A, size_t a, ActRegs &r) {
-    if (FMT == SLLM_Q5_0) {
+    if (act_f32(FMT)) {
         const float4 *src = (const float4 *)(A.xf + a * kXfStride);
 #pragma unroll
         for (int k = 0; k < 8; k++) r.xf[k] = src[k];
@@ -151,9 +166,54 @@ __device__ __forceinline__ void load_act(const ActView &A, size_t a, ActRegs &r)
 
 // Adds one block's term to acc (acc2: the Q5K1 high half), in the reference's
 // operation order for that format.
+// Element e (0..31) of a block's fp32 activations (e a compile-time constant).
+__device__ __forceinline__ float elem(const float4 *v, int e) {
+    const float4 t = v[e >> 2];
+    return (e & 3) == 0 ? t.x : ((e & 3) == 1 ? t.y : ((e & 3) == 2 ? t.z : t.w));
+}
+
 template <int FMT>
 __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x, float &acc, float &acc2) {
-    if (FMT == SLLM_Q5_0) {
+    if (FMT == SLLM_Q2K) {
+        // dequantizeQ2KNative (kquants.go:147-180) gives w = float32(d*sc*q -
+        // dmin*m); here both products are exact in float32 and the difference
+        // is rounded once, to the same float32. Then the dense loop's product
+        // x * w (modelMatmulFloatIntoF32, float32_ops.go:475-477), summed per block.
+        const float d = f16_exact((uint16_t)(b.sbw & 0xffffu)), dm = f16_exact((uint16_t)(b.sbw >> 16));
+        float sum = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const uint32_t sc = ((uint32_t)b.d >> (8 * h)) & 0xffu;
+            const float dl = d * (float)(sc & 0xfu), ml = dm * (float)(sc >> 4);
+            const uint32_t w = h ? b.c2.y : b.c2.x;
+#pragma unroll
+            for (int l = 0; l < 16; l++) {
+                const float q = (float)((w >> (2 * l)) & 3u);
+                const float wt = dl * q - ml;
+                sum = sum + elem(x.xf, 16 * h + l) * wt;
+            }
+        }
+        acc = acc + sum;
+    } else if (FMT == SLLM_Q3K) {
+        // dequantizeQ3KNative (kquants.go:183-245): w = float32(d*(sc-32)*(q -
+        // sub)), sub 4 unless the element's high-mask bit is set - an exact
+        // float32 product here. Then x * w as above.
+        const float d = f16_exact((uint16_t)(b.sbw & 0xffffu));
+        float sum = 0.0f;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float dl = d * (float)(int)(int8_t)(((uint32_t)b.d >> (8 * h)) & 0xffu);
+            const uint32_t w = h ? b.c2.y : b.c2.x;
+            const uint32_t hb = b.qh >> (16 * h);
+#pragma unroll
+            for (int l = 0; l < 16; l++) {
+                const int q = (int)((w >> (2 * l)) & 3u) - (((hb >> l) & 1u) ? 0 : 4);
+                const float wt = dl * (float)q;
+                sum = sum + elem(x.xf, 16 * h + l) * wt;
+            }
+        }
+        acc = acc + sum;
+    } else if (FMT == SLLM_Q5_0) {
         const float sum = q5_block_sum(b.q, b.qh, x.xf);
         const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`
         acc = acc + grp;
@@ -589,8 +649,9 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
 template <int FMT, int NB, int D, int MT, bool PAIR>
 sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
                      size_t lds, hipStream_t s) {
-    // hoisting needs room for the operands: not for Q5_0 (32 fp32 per block)
-    constexpr bool kCanHoist = FMT != SLLM_Q5_0 && NB * MT <= 4;
+    // hoisting needs room for the operands: fp32-activation formats hold 32
+    // floats per block (not for Q5_0, whose term needs more registers itself)
+    constexpr bool kCanHoist = act_f32(FMT) ? (kq_native(FMT) && NB * MT <= 2 && NB * D <= 2) : NB * MT <= 4;
     // lanes per activation block in the prologue: as many as the workgroup allows
     int tpb = 8;
     while (tpb > (S.norm_w ? 4 : 1) && (int64_t)M * G * tpb > W * 64) tpb >>= 1;

@@ -19,7 +19,15 @@ namespace sllm {
 //   d    f16 scale bits           (all formats)
 //   m    f16 min bits             (Q4_1, Q5K1 low block)
 //   dh   f16 scale of the Q5K1 high block (16 * d*sc, truncated separately)
-//   qh   u32 high bits, bit e = bit 4 of element e (Q5_0, Q5K1)
+//   qh   u32 high bits, bit e = bit 4 of element e (Q5_0, Q5K1); Q3K: bit e =
+//        the high-mask bit of element e
+// Native k-quants (Q2K, Q3K), per 32-element block b of a super-block (two
+// 16-element sub-blocks):
+//   q2   8 B: the 2-bit codes in element order (x: elements 0..15, y: 16..31,
+//        element l at bits 2l)
+//   d    u16: the two sub-blocks' scale bytes (Q2K: sc | m << 4 as stored;
+//        Q3K: the decoded 6-bit scales minus 32, as int8)
+//   sb   u32 per super-block: Q2K d | dmin << 16, Q3K d (f16 bits)
 struct Planes {
     const int4 *qs = nullptr;
     const int4 *qs2 = nullptr;
@@ -27,6 +35,8 @@ struct Planes {
     const uint16_t *m = nullptr;
     const uint16_t *dh = nullptr;
     const uint32_t *qh = nullptr;
+    const uint2 *q2 = nullptr;
+    const uint32_t *sb = nullptr;
 };
 
 struct MutPlanes {
@@ -36,7 +46,16 @@ struct MutPlanes {
     uint16_t *m = nullptr;
     uint16_t *dh = nullptr;
     uint32_t *qh = nullptr;
+    uint2 *q2 = nullptr;
+    uint32_t *sb = nullptr;
 };
+
+// Formats whose activations stay fp32 (no Q8_0 codes): Q5_0 and the native k-quants.
+__host__ __device__ constexpr bool act_f32(int fmt) {
+    return fmt == SLLM_Q5_0 || fmt == SLLM_Q2K || fmt == SLLM_Q3K;
+}
+// Native k-quant formats (256-element super-blocks).
+__host__ __device__ constexpr bool kq_native(int fmt) { return fmt == SLLM_Q2K || fmt == SLLM_Q3K; }
 
 // Bytes each format streams per 32-element block from the planes.
 inline int plane_block_bytes(int fmt) {
@@ -46,6 +65,23 @@ inline int plane_block_bytes(int fmt) {
     case SLLM_Q4_1: return 20;
     case SLLM_Q5_0: return 22;
     case SLLM_Q5K1: return 26;
+    case SLLM_Q2K: return 11;  // 10.5: 8 + 2 + 4 / 8 (rounded up)
+    case SLLM_Q3K: return 15;  // 14.5: 8 + 4 + 2 + 4 / 8 (rounded up)
+    }
+    return 0;
+}
+
+// Bytes the reference's Raw (or, native k-quants, the GGUF blocks) takes for
+// nb 32-element blocks.
+inline size_t raw_bytes_of(int fmt, int64_t nb) {
+    if (fmt == SLLM_Q2K) return (size_t)(nb / 8) * 84;
+    if (fmt == SLLM_Q3K) return (size_t)(nb / 8) * 110;
+    switch (fmt) {
+    case SLLM_Q8_0: return (size_t)nb * 34;
+    case SLLM_Q4_0: return (size_t)nb * 18;
+    case SLLM_Q4_1: return (size_t)nb * 20;
+    case SLLM_Q5_0: return (size_t)nb * 22;
+    case SLLM_Q5K1: return (size_t)nb * 40;
     }
     return 0;
 }
@@ -73,6 +109,7 @@ size_t carve_planes(int fmt, int64_t nblocks, void *base, MutPlanes *out);
 inline Planes as_const(const MutPlanes &p) {
     Planes c;
     c.qs = p.qs; c.qs2 = p.qs2; c.d = p.d; c.m = p.m; c.dh = p.dh; c.qh = p.qh;
+    c.q2 = p.q2; c.sb = p.sb;
     return c;
 }
 
@@ -138,6 +175,8 @@ sllm_status pack_from_raw(int fmt, const uint8_t *raw_dev, int rows, int G, cons
 sllm_status pack_from_gguf(uint32_t ggml_type, const uint8_t *raw_dev, int rows, int cols,
                            const MutPlanes &P, hipStream_t s);
 sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
+// GGUF super-block bytes of a native k-quant weight from its (host copy of the) planes.
+void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *out);
 
 // The attention section of one layer (forwardBlock, model_f32.go:398-466) on
 // device buffers; launch_attention checks nothing (the C entry does).

@@ -6,9 +6,13 @@
 //   Q6_K, IQ4_NL -> Q8_0    (fp64 dequant gguf.go:988-1015 / kquants.go:14-27,
 //                            then quantizeQ8Rows gguf.go:1080-1134)
 //   fp32 -> Q8_0            (quantizeQ8RowsF32, gguf.go:1136-1186)
+//   Q2_K, Q3_K kept native  (codes in element order, scale bytes, d / dmin),
+//                           where the reference goes to dense fp32 (gguf.go:907-911)
 // All arithmetic is the reference's: fp64 products (exact for these inputs),
 // IEEE fp64/fp32 division, round-half-away-from-zero, truncating f16 encode.
 #include <hip/hip_runtime.h>
+
+#include <cstring>
 
 #include "qmm_device.hpp"
 #include "qmm_internal.hpp"
@@ -28,6 +32,14 @@ size_t carve_planes(int fmt, int64_t nb, void *base, MutPlanes *out) {
     // of a plane must not run off the allocation.
     const size_t n = (size_t)nb + kPlanePadBlocks;
     MutPlanes p;
+    if (kq_native(fmt)) {
+        p.q2 = (uint2 *)take(n * 8);
+        if (fmt == SLLM_Q3K) p.qh = (uint32_t *)take(n * 4);
+        p.d = (uint16_t *)take(n * 2);
+        p.sb = (uint32_t *)take(n / 8 * 4);
+        if (out) *out = p;
+        return (off + 255) & ~(size_t)255;
+    }
     p.qs = (int4 *)take(n * 16);
     if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take(n * 16);
     if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take(n * 4);
@@ -269,6 +281,57 @@ __global__ void pack_f32_kernel(const float *__restrict__ w, int64_t nb, MutPlan
     }
 }
 
+// The 2-bit codes of block bi (0..7) of a Q2_K / Q3_K super-block, from its
+// 64 code bytes: sub-block pair bi covers elements 32 bi .. 32 bi + 31, half
+// n = bi / 4 of the bytes at bit pair 2 (bi % 4) - the element order of
+// dequantizeQ2KNative / dequantizeQ3KNative (kquants.go:147-245).
+__device__ __forceinline__ uint2 kq_codes(const uint8_t *qs, int bi) {
+    const int n = bi >> 2, sh = 2 * (bi & 3);
+    const uint8_t *q = qs + 32 * n;
+    uint32_t x = 0, y = 0;
+    for (int l = 0; l < 16; l++) {
+        x |= (uint32_t)((q[l] >> sh) & 3) << (2 * l);
+        y |= (uint32_t)((q[16 + l] >> sh) & 3) << (2 * l);
+    }
+    return make_uint2(x, y);
+}
+
+// Q2_K (84 B / 256: scales[16], qs[64], d, dmin) kept native.
+__global__ void pack_q2k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 84;
+        const int bi = (int)(b & 7);
+        P.q2[b] = kq_codes(sb + 16, bi);
+        P.d[b] = (uint16_t)(sb[2 * bi] | (sb[2 * bi + 1] << 8));
+        if (bi == 0) P.sb[b >> 3] = (uint32_t)ld16(sb + 80) | ((uint32_t)ld16(sb + 82) << 16);
+    }
+}
+
+// The 6-bit scale s (0..15) of a Q3_K super-block from its 12 packed bytes:
+// the unpacking of dequantizeQ3KNative (kquants.go:195-210) for one scale.
+__host__ __device__ inline int q3k_scale(const uint8_t *scb, int s) {
+    const int k = s >> 2, i = s & 3;
+    const int hi = (scb[8 + i] >> (2 * k)) & 3;
+    const int lo = (k & 1) ? scb[4 + i] : scb[i];
+    return ((k < 2) ? (lo & 0x0f) : (lo >> 4)) | (hi << 4);
+}
+
+// Q3_K (110 B / 256: hmask[32], qs[64], scales[12], d) kept native.
+__global__ void pack_q3k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 110;
+        const int bi = (int)(b & 7);
+        P.q2[b] = kq_codes(sb + 32, bi);
+        const int bit = 4 * (bi >> 2) + (bi & 3);  // the hmask bit of this block (m in the reference)
+        uint32_t h = 0;
+        for (int e = 0; e < 32; e++) h |= (uint32_t)((sb[e] >> bit) & 1) << e;
+        P.qh[b] = h;
+        const int s0 = q3k_scale(sb + 96, 2 * bi) - 32, s1 = q3k_scale(sb + 96, 2 * bi + 1) - 32;
+        P.d[b] = (uint16_t)((s0 & 0xff) | ((s1 & 0xff) << 8));
+        if (bi == 0) P.sb[b >> 3] = ld16(sb + 108);
+    }
+}
+
 inline int grid_for(int64_t nb) {
     int64_t g = (nb + 255) / 256;
     return g > 65536 ? 65536 : (int)(g < 1 ? 1 : g);
@@ -292,10 +355,56 @@ sllm_status pack_from_gguf(uint32_t t, const uint8_t *raw_dev, int rows, int col
     case 13: hipLaunchKernelGGL(pack_q5k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
     case 14: hipLaunchKernelGGL(pack_q6k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
     case 20: hipLaunchKernelGGL(pack_iq4nl_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    case 10: hipLaunchKernelGGL(pack_q2k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
+    case 11: hipLaunchKernelGGL(pack_q3k_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P); break;
     default: return set_error(SLLM_ERR_QTYPE, "pack_from_gguf: not a remapped type");
     }
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
+}
+
+void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *o) {
+    // inverse of pack_q2k_kernel / pack_q3k_kernel, one super-block at a time
+    const int per = fmt == SLLM_Q2K ? 84 : 110;
+    for (int64_t s = 0; s < nb / 8; s++) {
+        uint8_t *sb = o + s * per;
+        std::memset(sb, 0, (size_t)per);
+        uint8_t *qs = sb + (fmt == SLLM_Q2K ? 16 : 32);
+        int v[16];
+        for (int bi = 0; bi < 8; bi++) {
+            const int64_t b = s * 8 + bi;
+            const int n = bi >> 2, sh = 2 * (bi & 3);
+            for (int l = 0; l < 16; l++) {
+                qs[32 * n + l] |= (uint8_t)(((p.q2[b].x >> (2 * l)) & 3) << sh);
+                qs[32 * n + 16 + l] |= (uint8_t)(((p.q2[b].y >> (2 * l)) & 3) << sh);
+            }
+            if (fmt == SLLM_Q2K) {
+                sb[2 * bi] = (uint8_t)(p.d[b] & 0xff);
+                sb[2 * bi + 1] = (uint8_t)(p.d[b] >> 8);
+            } else {
+                const int bit = 4 * n + (bi & 3);
+                for (int e = 0; e < 32; e++) sb[e] |= (uint8_t)(((p.qh[b] >> e) & 1) << bit);
+                v[2 * bi] = (int)(int8_t)(p.d[b] & 0xff) + 32;
+                v[2 * bi + 1] = (int)(int8_t)(p.d[b] >> 8) + 32;
+            }
+        }
+        if (fmt == SLLM_Q2K) {
+            sb[80] = (uint8_t)(p.sb[s] & 0xff);
+            sb[81] = (uint8_t)((p.sb[s] >> 8) & 0xff);
+            sb[82] = (uint8_t)((p.sb[s] >> 16) & 0xff);
+            sb[83] = (uint8_t)(p.sb[s] >> 24);
+        } else {
+            uint8_t *scb = sb + 96;
+            for (int i = 0; i < 4; i++) {
+                scb[i] = (uint8_t)((v[i] & 0x0f) | ((v[8 + i] & 0x0f) << 4));
+                scb[4 + i] = (uint8_t)((v[4 + i] & 0x0f) | ((v[12 + i] & 0x0f) << 4));
+                scb[8 + i] = (uint8_t)((v[i] >> 4) | ((v[4 + i] >> 4) << 2) | ((v[8 + i] >> 4) << 4) |
+                                       ((v[12 + i] >> 4) << 6));
+            }
+            sb[108] = (uint8_t)(p.sb[s] & 0xff);
+            sb[109] = (uint8_t)((p.sb[s] >> 8) & 0xff);
+        }
+    }
 }
 
 sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s) {

@@ -33,11 +33,11 @@ REPO_ROOT = os.path.dirname(PKG_ROOT)
 LIB_PATH = os.path.join(PKG_ROOT, "libsllm_qmm.so")
 HEADER_PATH = os.path.join(REPO_ROOT, "include", "sllm_qmm.h")
 
-QTYPES = {"q8": 0, "q4": 1, "q4_1": 2, "q5": 3, "q5k1": 4}
+QTYPES = {"q8": 0, "q4": 1, "q4_1": 2, "q5": 3, "q5k1": 4, "q2k": 5, "q3k": 6}
 QTYPE_NAMES = {v: k for k, v in QTYPES.items()}
 RAW_BLOCK_BYTES = {"q8": 34, "q4": 18, "q4_1": 20, "q5": 22, "q5k1": 40}
 # Bytes the device planes hold (and a GEMV streams) per 32-element block.
-PLANE_BLOCK_BYTES = {"q8": 34, "q4": 18, "q4_1": 20, "q5": 22, "q5k1": 26}
+PLANE_BLOCK_BYTES = {"q8": 34, "q4": 18, "q4_1": 20, "q5": 22, "q5k1": 26, "q2k": 10.5, "q3k": 14.5}
 
 STATUS = {0: "SLLM_OK", 1: "SLLM_ERR_ARG", 2: "SLLM_ERR_QTYPE", 3: "SLLM_ERR_SHAPE",
           4: "SLLM_ERR_DEVICE", 5: "SLLM_ERR_OOM", 6: "SLLM_ERR_FORMAT"}
@@ -181,7 +181,7 @@ class DeviceWeight:
 
     @property
     def plane_bytes(self) -> int:
-        return self.rows * self.groups * PLANE_BLOCK_BYTES[self.qtype]
+        return int(self.rows * self.groups * PLANE_BLOCK_BYTES[self.qtype])
 
     @classmethod
     def from_quant(cls, w: QuantWeight) -> "DeviceWeight":
@@ -228,7 +228,8 @@ class DeviceWeight:
 
 
 def load_weight_f32_direct(ggml_type: int, raw, rows: int, cols: int) -> DeviceWeight:
-    """gguf.go:818-934 for the int8-kernel types (8, 2, 3, 6, 12, 13, 14, 20)."""
+    """gguf.go:818-934 for the int8-kernel types (8, 2, 3, 6, 12, 13, 14, 20), and Q2_K / Q3_K
+    (10, 11) kept native where the reference goes to dense float32 (gguf.go:907-911)."""
     return DeviceWeight.from_gguf(ggml_type, raw, rows, cols)
 
 

@@ -117,6 +117,26 @@ def q6k_blocks(seed: int, rows: int, cols: int) -> np.ndarray:
     return out.reshape(-1)
 
 
+def q2k_blocks(seed: int, rows: int, cols: int) -> np.ndarray:
+    """Random Q2_K tensor (84 B / 256): random scale and code bytes, d ~ U(1e-4, 1e-2),
+    dmin ~ U(1e-4, 5e-3)."""
+    nb = rows * cols // 256
+    out = np.zeros((nb, 84), np.uint8)
+    out[:, 0:80] = random_bytes(seed, nb * 80).reshape(nb, 80)
+    _put16(out, 80, _f16_bits(1e-4 + uniform(seed + 1, nb) * (1e-2 - 1e-4)))
+    _put16(out, 82, _f16_bits(1e-4 + uniform(seed + 2, nb) * (5e-3 - 1e-4)))
+    return out.reshape(-1)
+
+
+def q3k_blocks(seed: int, rows: int, cols: int) -> np.ndarray:
+    """Random Q3_K tensor (110 B / 256): random mask, code and scale bytes, d ~ U(1e-4, 1e-2)."""
+    nb = rows * cols // 256
+    out = np.zeros((nb, 110), np.uint8)
+    out[:, 0:108] = random_bytes(seed, nb * 108).reshape(nb, 108)
+    _put16(out, 108, _f16_bits(1e-4 + uniform(seed + 1, nb) * (1e-2 - 1e-4)))
+    return out.reshape(-1)
+
+
 def iq4nl_blocks(seed: int, rows: int, cols: int) -> np.ndarray:
     """Random IQ4_NL tensor (18 B / 32)."""
     nb = rows * cols // 32
@@ -179,6 +199,7 @@ def quantize_q5_0(w: np.ndarray) -> np.ndarray:
 # GGUF tensor type ids used by the BASELINE configs.
 GGML_Q4_0, GGML_Q4_1, GGML_Q5_0, GGML_Q8_0 = 2, 3, 6, 8
 GGML_Q4_K, GGML_Q5_K, GGML_Q6_K, GGML_IQ4_NL = 12, 13, 14, 20
+GGML_Q2_K, GGML_Q3_K = 10, 11
 
 BLOCKS = {GGML_Q4_K: q4k_blocks, GGML_Q5_K: q5k_blocks, GGML_Q6_K: q6k_blocks, GGML_IQ4_NL: iq4nl_blocks}
 

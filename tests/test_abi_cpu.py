@@ -41,7 +41,9 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_weight_from_quant(b"q8", p, raw.nbytes, 2, 4, 32, C.byref(h)) == 1      # groups != cols/32
     assert lib.sllm_weight_from_quant(b"q8", p, 10, 1, 4, 32, C.byref(h)) == 1              # Raw too short
     assert lib.sllm_weight_from_quant(b"q8", None, 10, 1, 4, 32, C.byref(h)) == 1           # null Raw
-    assert lib.sllm_weight_from_gguf(10, p, raw.nbytes, 4, 256, C.byref(h)) == 2            # Q2_K: dense in the reference
+    assert lib.sllm_weight_from_gguf(7, p, raw.nbytes, 4, 256, C.byref(h)) == 2             # Q5_1: dense in the reference
+    assert lib.sllm_weight_from_gguf(10, p, raw.nbytes, 4, 128, C.byref(h)) == 3            # Q2_K needs cols % 256
+    assert lib.sllm_weight_from_gguf(11, p, 16, 1, 256, C.byref(h)) == 1                    # Q3_K: too short
     assert lib.sllm_weight_from_gguf(12, p, raw.nbytes, 4, 128, C.byref(h)) == 3            # Q4_K needs cols % 256
     assert lib.sllm_weight_from_gguf(12, p, 16, 1, 256, C.byref(h)) == 1                    # too short
     assert lib.sllm_matmul_quant_into_f32(None, p, 1, 32, p) == 1

@@ -87,7 +87,7 @@ def test_gguf_load_bitexact(ggml_type, expect):
 
 def test_gguf_unsupported_type():
     with pytest.raises(sq.SllmError) as e:
-        sq.load_weight_f32_direct(10, np.zeros(84 * 4, np.uint8), 4, 256)  # Q2_K: dense fp32 in the reference
+        sq.load_weight_f32_direct(7, np.zeros(24 * 32, np.uint8), 4, 256)  # Q5_1: dense fp32 in the reference
     assert e.value.status == 2
 
 
