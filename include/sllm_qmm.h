@@ -110,6 +110,17 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
                              size_t *raw_bytes);
 
 /*
+ * Bytes one decode GEMV of this weight streams from HBM (its planes as the
+ * kernel reads them: the algorithmic weight bytes of a matmul). With the
+ * tuning knob "gemv_q4k_stream" set, Q4_K weights stream the Q4_1 nibbles
+ * and the GGUF Q4_K headers, 18 B per 32 weights (the Q4_1 scale and min
+ * rebuilt in the kernel as convertQ4KToQ41 computes them,
+ * kquant_kernels.go:30-63); by default they stream the Q4_1 planes (20 B),
+ * which measures faster. No counterpart in the reference.
+ */
+sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes);
+
+/*
  * Rebuild the reference Raw bytes (QuantWeight.Raw layout) from the device
  * planes into host memory (cap >= raw_bytes). Bit-exact inverse of the repack.
  * SLLM_Q2K / SLLM_Q3K: the GGUF super-block bytes the weight was made from.

@@ -13,7 +13,8 @@
 #include "qmm_internal.hpp"
 
 struct sllm_weight {
-    int fmt = 0;
+    int fmt = 0;     // the QType at the ABI
+    int layout = 0;  // the plane layout (SLLM_Q4K_STREAM: Q4_1 planes + the Q4_K headers)
     int groups = 0, rows = 0, cols = 0;
     int device = 0;
     void *base = nullptr;
@@ -197,21 +198,22 @@ int parse_qtype(const char *q) {
     return -1;
 }
 
-sllm_status alloc_weight(int fmt, int rows, int cols, sllm_weight **out) {
+sllm_status alloc_weight(int fmt, int rows, int cols, sllm_weight **out, int layout = -1) {
     auto *w = new sllm_weight();
     w->fmt = fmt;
+    w->layout = layout < 0 ? fmt : layout;
     w->rows = rows;
     w->cols = cols;
     w->groups = cols / 32;
     (void)hipGetDevice(&w->device);
     const int64_t nb = (int64_t)rows * w->groups;
-    w->bytes = carve_planes(fmt, nb, nullptr, nullptr);
+    w->bytes = carve_planes(w->layout, nb, nullptr, nullptr);
     hipError_t e = hipMalloc(&w->base, w->bytes);
     if (e != hipSuccess) {
         delete w;
         return set_error(SLLM_ERR_OOM, "weight plane allocation failed");
     }
-    carve_planes(fmt, nb, w->base, &w->planes);
+    carve_planes(w->layout, nb, w->base, &w->planes);
     *out = w;
     return SLLM_OK;
 }
@@ -236,12 +238,18 @@ bool uses_gemm(const sllm_weight *w, int x_rows) {
     return x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups);
 }
 
+// The GEMV kernel format of a weight: Q4_K weights stream their GGUF headers
+// (unless the tuning knob says otherwise), every other weight its QType's planes.
+int gemv_fmt(const sllm_weight *w) {
+    return (w->layout == SLLM_Q4K_STREAM && tuning().gemv_q4k_stream) ? SLLM_Q4K_STREAM : w->fmt;
+}
+
 // One weight's matmul on device buffers: the GEMV, or the GEMM with the given
 // activation workspace (at least gemm_workspace_bytes).
 sllm_status run_matmul(const sllm_weight *w, const float *x, int x_rows, float *dst, hipStream_t s, void *ws,
                        size_t cap) {
     const Planes P = as_const(w->planes);
-    if (!uses_gemm(w, x_rows)) return launch_gemv(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    if (!uses_gemm(w, x_rows)) return launch_gemv(gemv_fmt(w), P, x, dst, w->rows, w->groups, x_rows, s);
     return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
 }
 
@@ -278,21 +286,21 @@ sllm_status multi_impl(const sllm_weight *const *ws, int count, const float *x, 
         int N[kMaxSegs];
         int n = 0;
         for (int j = i; j < count && n < kMaxSegs; j++) {
-            if (done[(size_t)j] || ws[j]->fmt != w->fmt || uses_gemm(ws[j], x_rows)) continue;
+            if (done[(size_t)j] || gemv_fmt(ws[j]) != gemv_fmt(w) || uses_gemm(ws[j], x_rows)) continue;
             P[n] = as_const(ws[j]->planes);
             D[n] = dst[j];
             N[n] = ws[j]->rows;
             n++;
             done[(size_t)j] = 1;
         }
-        if ((st = launch_gemv_multi(w->fmt, P, D, N, n, x, w->groups, x_rows, s, nw, eps)) != SLLM_OK) return st;
+        if ((st = launch_gemv_multi(gemv_fmt(w), P, D, N, n, x, w->groups, x_rows, s, nw, eps)) != SLLM_OK) return st;
     }
     return SLLM_OK;
 }
 
 // Whether gate / up fit the one paired GEMV launch.
 bool swiglu_paired(const sllm_weight *wg, const sllm_weight *wu, int x_rows) {
-    return !uses_gemm(wg, x_rows) && !uses_gemm(wu, x_rows) && wg->fmt == wu->fmt;
+    return !uses_gemm(wg, x_rows) && !uses_gemm(wu, x_rows) && gemv_fmt(wg) == gemv_fmt(wu);
 }
 
 // Workspace the unpaired SwiGLU path needs: the GEMM workspace, then gate / up
@@ -309,7 +317,7 @@ sllm_status swiglu_impl(const sllm_weight *wg, const sllm_weight *wu, const floa
                         float *gate, float *up, hipStream_t s, void *ws, const float *nw, float eps) {
     const int N = wg->rows;
     if (swiglu_paired(wg, wu, x_rows))
-        return launch_gemv_swiglu(wg->fmt, as_const(wg->planes), as_const(wu->planes), x, h, gate, up, N,
+        return launch_gemv_swiglu(gemv_fmt(wg), as_const(wg->planes), as_const(wu->planes), x, h, gate, up, N,
                                   wg->groups, x_rows, s, nw, eps);
     // Prefill or mixed formats: the two matmuls, then the elementwise SwiGLU;
     // x is already normed here (nw is only passed for the paired launch).
@@ -406,6 +414,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemv_inflight_kb") && value >= 64) t.gemv_inflight_kb = value;
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
+    else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;
 }
@@ -449,14 +458,14 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     *out = nullptr;
     sllm_status st = SLLM_OK;
     if (!check_shape(rows, cols, &st)) return st;
-    int fmt = -1;
+    int fmt = -1, layout = -1;
     size_t per = 0, blk = 32;
     switch (t) {
     case 8: fmt = SLLM_Q8_0; per = 34; break;
     case 2: fmt = SLLM_Q4_0; per = 18; break;
     case 3: fmt = SLLM_Q4_1; per = 20; break;
     case 6: fmt = SLLM_Q5_0; per = 22; break;
-    case 12: fmt = SLLM_Q4_1; per = 144; blk = 256; break;
+    case 12: fmt = SLLM_Q4_1; per = 144; blk = 256; layout = SLLM_Q4K_STREAM; break;
     case 13: fmt = SLLM_Q5K1; per = 176; blk = 256; break;
     case 14: fmt = SLLM_Q8_0; per = 210; blk = 256; break;
     case 20: fmt = SLLM_Q8_0; per = 18; break;
@@ -471,7 +480,7 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     if (raw_bytes < need) return set_error(SLLM_ERR_ARG, "raw is shorter than the tensor's blocks");
     if ((st = ensure_init()) != SLLM_OK) return st;
     sllm_weight *w = nullptr;
-    if ((st = alloc_weight(fmt, rows, cols, &w)) != SLLM_OK) return st;
+    if ((st = alloc_weight(fmt, rows, cols, &w, layout)) != SLLM_OK) return st;
     st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
         const uint8_t *dev = (const uint8_t *)c->buf;
         if (t == 8 || t == 2 || t == 3 || t == 6) return pack_from_raw(fmt, dev, rows, cols / 32, w->planes, nullptr, c->stream);
@@ -521,6 +530,12 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
     return SLLM_OK;
 }
 
+sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes) {
+    if (!w || !bytes) return set_error(SLLM_ERR_ARG, "null pointer");
+    *bytes = stream_bytes_of(gemv_fmt(w), (int64_t)w->rows * w->groups);
+    return SLLM_OK;
+}
+
 sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap) {
     if (!w || !raw) return set_error(SLLM_ERR_ARG, "null pointer");
     const int64_t nb = (int64_t)w->rows * w->groups;
@@ -529,7 +544,7 @@ sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap) {
     std::vector<unsigned char> img(w->bytes);
     SLLM_HIP(hipMemcpy(img.data(), w->base, w->bytes, hipMemcpyDeviceToHost));
     MutPlanes p;
-    carve_planes(w->fmt, nb, img.data(), &p);
+    carve_planes(w->layout, nb, img.data(), &p);
     if (kq_native(w->fmt)) {
         export_kq_native(w->fmt, p, nb, (uint8_t *)raw);
         return SLLM_OK;
@@ -600,7 +615,7 @@ sllm_status sllm_matmul_argmax_dev(const sllm_weight *w, const float *x, int x_c
     hipStream_t s = (hipStream_t)stream;
     void *scr = nullptr;
     if ((st = amax_scratch(s, &scr)) != SLLM_OK) return st;
-    return launch_gemv_argmax(w->fmt, as_const(w->planes), x, logits, w->rows, w->groups,
+    return launch_gemv_argmax(gemv_fmt(w), as_const(w->planes), x, logits, w->rows, w->groups,
                               (unsigned long long *)scr, (unsigned int *)((char *)scr + 8), argmax, s);
 }
 
@@ -767,7 +782,7 @@ sllm_status sllm_rmsnorm_matmul_argmax_dev(const sllm_weight *w, const float *x,
     hipStream_t s = (hipStream_t)stream;
     void *scr = nullptr;
     if ((st = amax_scratch(s, &scr)) != SLLM_OK) return st;
-    return launch_gemv_argmax(w->fmt, as_const(w->planes), x, logits, w->rows, w->groups,
+    return launch_gemv_argmax(gemv_fmt(w), as_const(w->planes), x, logits, w->rows, w->groups,
                               (unsigned long long *)scr, (unsigned int *)((char *)scr + 8), argmax, s, norm_w, eps);
 }
 
@@ -891,7 +906,7 @@ sllm_status sllm_matmul_add_dev(const sllm_weight *w, const float *x, int x_rows
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
     const Planes P = as_const(w->planes);
-    if (!uses_gemm(w, x_rows)) return launch_gemv_add(w->fmt, P, x, dst, w->rows, w->groups, x_rows, s);
+    if (!uses_gemm(w, x_rows)) return launch_gemv_add(gemv_fmt(w), P, x, dst, w->rows, w->groups, x_rows, s);
     // GEMM: the product into the workspace behind the GEMM's own, then dst += it
     const size_t gb = align256(gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows));
     const size_t n = (size_t)x_rows * w->rows;

@@ -43,6 +43,31 @@ __device__ __forceinline__ uint16_t f64_to_f16_trunc(double f) {
     return sign | (uint16_t)(exp16 << 10) | (uint16_t)((bits >> 42) & 0x3ffu);
 }
 
+// float64ToFloat16 of a value that float32 holds exactly (so its top mantissa
+// bits and exponent are the fp64 value's): the same truncating encode.
+__device__ __forceinline__ uint16_t f32_to_f16_trunc(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    const uint32_t sign = (u >> 16) & 0x8000u;
+    const int e = (int)((u >> 23) & 0xffu);
+    if (e == 0xff) return 0;  // NaN or Inf
+    const int e16 = e - 127 + 15;
+    if (e == 0 || e16 <= 0) return (uint16_t)sign;
+    if (e16 >= 0x1f) return (uint16_t)(sign | 0x7c00u);
+    return (uint16_t)(sign | ((uint32_t)e16 << 10) | ((u >> 13) & 0x3ffu));
+}
+
+// f16_exact(f32_to_f16_trunc(f)) without the round trip: the f16 normal range
+// keeps the top 10 mantissa bits, below it a signed zero, above it a signed
+// Inf, NaN / Inf give +0.
+__device__ __forceinline__ float f16_trunc_value(float f) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    const uint32_t e = (u >> 23) & 0xffu;
+    const uint32_t sign = u & 0x80000000u;
+    uint32_t r = (e >= 113u && e <= 142u) ? (u & 0xffffe000u) : (e > 142u ? (sign | 0x7f800000u) : sign);
+    r = e == 0xffu ? 0u : r;
+    return __builtin_bit_cast(float, r);
+}
+
 // ------------------------------------------------- activation quantizer ----
 
 // Combine a value across the TPB consecutive, aligned lanes that share a block

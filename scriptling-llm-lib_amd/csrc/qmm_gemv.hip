@@ -29,6 +29,10 @@ extern template sllm_status launch_mt<SLLM_Q5K1, false>(int, int, int, const Seg
                                                           int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q5K1, true>(int, int, int, const SegTable &, const float *, int, int, int,
                                                           int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4K_STREAM, false>(int, int, int, const SegTable &, const float *, int, int,
+                                                                int, int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q4K_STREAM, true>(int, int, int, const SegTable &, const float *, int, int,
+                                                               int, int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q2K, false>(int, int, int, const SegTable &, const float *, int, int, int,
                                                          int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q2K, true>(int, int, int, const SegTable &, const float *, int, int, int,
@@ -168,6 +172,7 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         case SLLM_Q4_1: st = SLLM_GEMV_FMT(SLLM_Q4_1); break;
         case SLLM_Q5_0: st = SLLM_GEMV_FMT(SLLM_Q5_0); break;
         case SLLM_Q5K1: st = SLLM_GEMV_FMT(SLLM_Q5K1); break;
+        case SLLM_Q4K_STREAM: st = SLLM_GEMV_FMT(SLLM_Q4K_STREAM); break;
         case SLLM_Q2K: st = SLLM_GEMV_FMT(SLLM_Q2K); break;
         case SLLM_Q3K: st = SLLM_GEMV_FMT(SLLM_Q3K); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");

@@ -110,6 +110,8 @@ struct BlockRegs {
     uint32_t qh;
     uint2 c2;      // native k-quants: the 2-bit codes
     uint32_t sbw;  // native k-quants: the super-block's scale word
+    int4 hq;       // Q4_K streamed: the super-block's GGUF header
+    uint32_t jj;   // Q4_K streamed: the block's index in its super-block
 };
 
 template <class T>
@@ -128,6 +130,11 @@ __device__ __forceinline__ void load_block(const Planes &P, uint32_t idx, BlockR
         return;
     }
     b.q = ld_nt(at(P.qs, idx));
+    if (FMT == SLLM_Q4K_STREAM) {
+        b.hq = ld_nt(at(P.hdr, idx >> 3));  // rows hold whole super-blocks (G % 8 == 0)
+        b.jj = idx & 7u;
+        return;
+    }
     b.d = ld_nt(at(P.d, idx));
     if (FMT == SLLM_Q8_0) b.q2 = ld_nt(at(P.qs2, idx));
     if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) b.m = ld_nt(at(P.m, idx));
@@ -213,6 +220,30 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
             }
         }
         acc = acc + sum;
+    } else if (FMT == SLLM_Q4K_STREAM) {
+        // convertQ4KToQ41 (kquant_kernels.go:30-63) for this block: scale / min
+        // pair jj of getScaleMinK4 (kquants.go:62-71), d' = float64ToFloat16(d *
+        // sc), m' = float64ToFloat16(-dmin * m) - both products exact in float32,
+        // so the truncating encode sees the fp64 value - then the Q4_1 term.
+        const uint32_t jj = b.jj, k8 = 8 * (jj & 3u);
+        const uint32_t A = ((uint32_t)b.hq.y >> k8) & 0xffu;  // scale byte jj & 3
+        const uint32_t B = ((uint32_t)b.hq.z >> k8) & 0xffu;  // byte (jj & 3) + 4
+        const uint32_t C = ((uint32_t)b.hq.w >> k8) & 0xffu;  // byte (jj & 3) + 8
+        const bool lo = jj < 4;
+        const uint32_t sc = lo ? (A & 63u) : ((C & 15u) | ((A >> 6) << 4));
+        const uint32_t mn = lo ? (B & 63u) : ((C >> 4) | ((B >> 6) << 4));
+        const float d = f16_exact((uint16_t)((uint32_t)b.hq.x & 0xffffu));
+        const float dmin = f16_exact((uint16_t)((uint32_t)b.hq.x >> 16));
+        const float dq = f16_trunc_value(d * (float)sc);
+        const float mq = f16_trunc_value(-dmin * (float)mn);
+        // q41q8_row_amd64.s:65-71: ((float(qsum)*d) + (float(Σxq)*m)) * xs
+        const float fsx = (float)x.sx;
+        const int qsum = nib_isum(b.q, x.xl, x.xh);
+        const float t1 = (float)qsum * dq;
+        const float t2 = fsx * mq;
+        float t = t1 + t2;
+        t = t * x.xs;
+        acc = acc + t;
     } else if (FMT == SLLM_Q5_0) {
         const float sum = q5_block_sum(b.q, b.qh, x.xf);
         const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`

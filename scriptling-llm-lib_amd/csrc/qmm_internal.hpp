@@ -28,6 +28,8 @@ namespace sllm {
 //   d    u16: the two sub-blocks' scale bytes (Q2K: sc | m << 4 as stored;
 //        Q3K: the decoded 6-bit scales minus 32, as int8)
 //   sb   u32 per super-block: Q2K d | dmin << 16, Q3K d (f16 bits)
+//   hdr  16 B per super-block (Q4_K streamed natively): the GGUF Q4_K header
+//        (d, dmin, the 12 packed scale bytes), next to the Q4_1 planes
 struct Planes {
     const int4 *qs = nullptr;
     const int4 *qs2 = nullptr;
@@ -37,6 +39,7 @@ struct Planes {
     const uint32_t *qh = nullptr;
     const uint2 *q2 = nullptr;
     const uint32_t *sb = nullptr;
+    const int4 *hdr = nullptr;
 };
 
 struct MutPlanes {
@@ -48,7 +51,15 @@ struct MutPlanes {
     uint32_t *qh = nullptr;
     uint2 *q2 = nullptr;
     uint32_t *sb = nullptr;
+    int4 *hdr = nullptr;
 };
+
+// Kernel format of a Q4_K weight streamed natively: the Q4_1 nibble plane plus
+// the GGUF header per super-block (18 B / 32 weights); the Q4_1 scale and min
+// of each block are rebuilt in the kernel (convertQ4KToQ41's arithmetic).
+// Internal only: such a weight is a "q4_1" QuantWeight at the ABI (its d / m
+// planes serve the GEMM and the export).
+constexpr int SLLM_Q4K_STREAM = 7;
 
 // Formats whose activations stay fp32 (no Q8_0 codes): Q5_0 and the native k-quants.
 __host__ __device__ constexpr bool act_f32(int fmt) {
@@ -65,10 +76,19 @@ inline int plane_block_bytes(int fmt) {
     case SLLM_Q4_1: return 20;
     case SLLM_Q5_0: return 22;
     case SLLM_Q5K1: return 26;
+    case SLLM_Q4K_STREAM: return 18;  // 16 + 16 / 8
     case SLLM_Q2K: return 11;  // 10.5: 8 + 2 + 4 / 8 (rounded up)
     case SLLM_Q3K: return 15;  // 14.5: 8 + 4 + 2 + 4 / 8 (rounded up)
     }
     return 0;
+}
+
+// Bytes one GEMV streams from the planes of nb blocks (the algorithmic weight bytes).
+inline size_t stream_bytes_of(int fmt, int64_t nb) {
+    if (fmt == SLLM_Q2K) return (size_t)nb * 10 + (size_t)(nb / 8) * 4;
+    if (fmt == SLLM_Q3K) return (size_t)nb * 14 + (size_t)(nb / 8) * 4;
+    if (fmt == SLLM_Q4K_STREAM) return (size_t)nb * 16 + (size_t)(nb / 8) * 16;
+    return (size_t)nb * plane_block_bytes(fmt);
 }
 
 // Bytes the reference's Raw (or, native k-quants, the GGUF blocks) takes for
@@ -109,7 +129,7 @@ size_t carve_planes(int fmt, int64_t nblocks, void *base, MutPlanes *out);
 inline Planes as_const(const MutPlanes &p) {
     Planes c;
     c.qs = p.qs; c.qs2 = p.qs2; c.d = p.d; c.m = p.m; c.dh = p.dh; c.qh = p.qh;
-    c.q2 = p.q2; c.sb = p.sb;
+    c.q2 = p.q2; c.sb = p.sb; c.hdr = p.hdr;
     return c;
 }
 
@@ -209,6 +229,7 @@ struct Tuning {
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
+    int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
     int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
 };
 Tuning &tuning();

@@ -44,7 +44,8 @@ size_t carve_planes(int fmt, int64_t nb, void *base, MutPlanes *out) {
     if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take(n * 16);
     if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take(n * 4);
     p.d = (uint16_t *)take(n * 2);
-    if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1) p.m = (uint16_t *)take(n * 2);
+    if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1 || fmt == SLLM_Q4K_STREAM) p.m = (uint16_t *)take(n * 2);
+    if (fmt == SLLM_Q4K_STREAM) p.hdr = (int4 *)take(n / 8 * 16);
     if (fmt == SLLM_Q5K1) p.dh = (uint16_t *)take(n * 2);
     if (out) *out = p;
     return (off + 255) & ~(size_t)255;
@@ -188,6 +189,7 @@ __global__ void pack_q4k_kernel(const uint8_t *__restrict__ raw, int64_t nb, Mut
         const uint8_t *sb = raw + (b >> 3) * 144;
         double dsc;
         kquant_low_block(sb, sb + 16, (int)(b & 7), P.qs[b], P.d[b], P.m[b], dsc);
+        if (P.hdr && (b & 7) == 0) P.hdr[b >> 3] = ld_int4(sb);  // d, dmin, scales[12]
     }
 }
 

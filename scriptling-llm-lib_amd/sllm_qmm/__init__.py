@@ -103,6 +103,7 @@ def lib() -> C.CDLL:
     L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
     L.sllm_set_param.argtypes = [C.c_char_p, i32]
     L.sllm_matmul_add_dev.argtypes = [W, P, i32, i32, P, P]
+    L.sllm_weight_stream_bytes.argtypes = [W, C.POINTER(sz)]
     L.sllm_kv_cache_create.argtypes = [i32, i32, i32, i32, C.POINTER(P)]
     L.sllm_kv_cache_destroy.argtypes = [P]
     L.sllm_kv_cache_length.argtypes = [P, i32, C.POINTER(i32)]
@@ -181,7 +182,10 @@ class DeviceWeight:
 
     @property
     def plane_bytes(self) -> int:
-        return int(self.rows * self.groups * PLANE_BLOCK_BYTES[self.qtype])
+        """Bytes one GEMV streams from this weight's planes (sllm_weight_stream_bytes)."""
+        n = C.c_size_t()
+        _check(lib().sllm_weight_stream_bytes(self.handle, C.byref(n)))
+        return n.value
 
     @classmethod
     def from_quant(cls, w: QuantWeight) -> "DeviceWeight":
