@@ -585,12 +585,14 @@ def decode_full_step(sq, torch, stream, layer_ws, head, nw, eps, xh, tokens: int
         res[f"decode_full_graph_matches_eager_kv{pos}"] = same
         res[f"attention_us_per_layer_kv{pos}"] = round(att_us, 2)
         res[f"attention_kv_GBps_kv{pos}"] = round(kv_bytes / (att_us * 1e-6) / 1e9, 1)
-    res["decode_full_note"] = ("whole step on the device: 32 x [RMSNorm+qkv, attention (prep + split-K "
-                               "kernel), o + residual, RMSNorm+gate/up+SwiGLU, down + residual] + RMSNorm+head+"
-                               "argmax, + one embedding-row copy: 193 launches per token at KV position pos "
+    res["decode_full_note"] = ("whole step on the device: 32 x [RMSNorm+qkv, attention (split kernel with the "
+                               "q/k preparation and the cache append, + a combine launch when the positions "
+                               "are split over workgroups: at KV 2047, not at KV 128), o + residual, "
+                               "RMSNorm+gate/up+SwiGLU, down + residual] + RMSNorm+head+argmax, + one "
+                               "embedding-row copy: 161 launches per token at KV 128, 193 at KV 2047 "
                                "(Llama-3-8B shape: 32 q heads, 8 kv heads, d_k 128, RoPE base 500000), replayed "
                                "from a HIP graph (the GPU-side cost); _eager: the same calls issued from Python "
-                               "(host-bound). attention_us_per_layer: the two attention launches of one layer "
+                               "(host-bound). attention_us_per_layer: the attention launches of one layer "
                                "(graph of the 32 layers' calls); attention_kv_GBps: K and V bytes read per layer "
                                "over that time")
     kvc.close()

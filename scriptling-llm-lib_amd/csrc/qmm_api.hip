@@ -413,6 +413,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemv_max_nb") && value >= 1 && value <= 8) t.gemv_max_nb = value;
     else if (!std::strcmp(name, "gemv_inflight_kb") && value >= 64) t.gemv_inflight_kb = value;
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
+    else if (!std::strcmp(name, "attn_tile_groups") && value >= 1 && value <= 4) t.attn_tile_groups = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
@@ -1004,9 +1005,9 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     sllm_status st = ensure_init();
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    int splits = 0, tps = 0;
+    int splits = 0, tps = 0, tw = 0;
     size_t wsb = 0;
-    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &wsb);
+    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &wsb);
     void *ws = nullptr;
     size_t cap = 0;
     if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
@@ -1042,6 +1043,7 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     a.part = (float *)((char *)ws + align256((size_t)seq_len * p->n_heads * kv->d_k * sizeof(float)));
     a.splits = splits;
     a.tps = tps;
+    a.tw = tw;
     if ((st = launch_attention(a, s)) != SLLM_OK) return st;
     kv->len[(size_t)layer] = cl + seq_len;
     return SLLM_OK;

@@ -3,17 +3,20 @@
 // RoPE, the KV-cache append and the causal GQA attention with merged heads.
 //
 // attn_split_kernel: one workgroup per (split, row, kv head). A split is a
-//   range of cached positions in tiles of 64 (one per lane); the workgroup
-//   stages a tile's K and V rows in LDS once for all q heads of the group
-//   (GQA: the kv head is read from HBM once), each wave owns one q head,
-//   and the split's partial softmax state goes to the workspace.
-//   Scores are the reference's sequential float32 dots. For one query row
-//   (decode) it also does the bias / norm / RoPE / append work itself.
+//   range of cached positions in tiles of 64 (one per lane), shared by up to
+//   four tile groups of waves that run side by side; a group stages its
+//   tile's K and V rows in LDS once for all q heads of the kv group (GQA:
+//   the kv head is read from HBM once) and each of its waves owns one q
+//   head. The groups' softmax states are merged in LDS; with one split the
+//   workgroup writes the attention output itself, otherwise the split's
+//   state goes to the workspace. Scores are the reference's sequential
+//   float32 dots. For one query row (decode) it also does the bias / norm /
+//   RoPE / append work itself.
 // attn_prep_kernel (several rows): that work, one wave per (row, head).
-// attn_combine_kernel: one wave per (row, head) merges the splits. Separate
-//   launches instead of a last-workgroup combine: on this multi-XCD part a
-//   device-scope fence writes back and invalidates the L2, which costs more
-//   than the launch.
+// attn_combine_kernel (more than one split): one wave per (row, head) merges
+//   the splits. Separate launches instead of a last-workgroup combine: on
+//   this multi-XCD part a device-scope fence writes back and invalidates the
+//   L2, which costs more than the launch.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -28,10 +31,13 @@ namespace {
 constexpr int kTile = 64;     // positions per tile: one per lane
 constexpr int kChunk = 128;   // K columns staged per pass (LDS: 64 x 132 floats)
 constexpr int kMaxDk = 256;   // head size limit (o: 4 values per lane)
+constexpr int kMaxWaves = 12; // split workgroup: up to three tile groups of four waves (168 VGPRs each)
+constexpr int kDotSteps = 4;  // 4-element steps of a score's LDS reads issued together
 
 // Native 4-float vector: arrays of it stay in registers (HIP's float4, a
 // union type, can keep a register array in scratch memory).
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v2f __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float lane_bcast(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
@@ -114,84 +120,112 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
 // fusedAttentionHeadF32 (float32_ops.go:190-235) for the q heads of one kv
 // head (repeatKVDataF32, float32_ops.go:252-260: q head g*rep + r reads kv
 // head g) and one query row, over one split of the positions the causal mask
-// leaves (0 .. cache_len + qi): writes the split's running max, sum of
-// exponentials and exponential-weighted sum of values per head. Score =
-// (sequential float32 dot) * scale, as the reference computes it; the
-// exponentials are float32(exp(float64(score - running max))), rescaled by
-// the same form when the running max grows.
+// leaves (0 .. cache_len + qi). Score = (sequential float32 dot) * scale, as
+// the reference computes it; the exponentials are float32(exp(float64(score
+// - running max))), rescaled by the same form when the running max grows.
 //
-// Wave r owns q head r of the group (max(4, rep) waves); lane l holds the
-// values d = l + 64 j, j < DKL (DKL = d_k / 64 rounded up). PREP (one query
-// row): the waves first build their q heads (bias, norm, RoPE) in LDS, and
-// the workgroup whose range holds the new position builds the new k / v row,
-// appends it to the cache and uses it from LDS; otherwise attn_prep_kernel
-// has done both. Per tile the K and V rows are loaded together (K straight
-// to LDS, V to registers while the scores are computed, then to the same LDS
-// buffer): one memory latency per tile, overlapped with the q preparation
-// for the first. LDS reads are issued in groups of eight.
-template <bool PREP, int DKL>
-__global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
+// The split is a.tw tile groups of nh = max(4, rep) waves (at most
+// kMaxWaves waves in all); group t takes
+// a.tps consecutive tiles of the split's range (every group runs the same
+// number of steps, so the workgroup barriers line up; a tile past the range
+// has no positions). Wave r of a group owns q head r; lane l holds the
+// values d = l + 64 j, j < DKL (DKL = d_k / 64 rounded up; FULL: d_k is
+// exactly 64 DKL, one K chunk). PREP (one query
+// row): group 0's waves first build the q heads (bias, norm, RoPE) in LDS,
+// and in the workgroup whose range holds the new position the last wave
+// builds the new k / v row, appends it to the cache and the groups use it
+// from LDS; otherwise attn_prep_kernel has done both. Per tile the K and V
+// rows are loaded together (K straight to LDS, V to registers while the
+// scores are computed, then to the same LDS buffer): one memory latency per
+// tile, overlapped with the q preparation for the first (whose V rows are
+// issued after that preparation). LDS reads are
+// issued in groups. At the end each wave leaves its (max, sum,
+// values) state in LDS and group 0 merges the groups' states in group order
+// exactly as attn_combine_kernel merges splits.
+template <bool PREP, int DKL, bool FULL>
+__global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) {
 
     extern __shared__ __attribute__((aligned(16))) float lds[];
     constexpr int ks = kChunk + 4;
-    float *kt = lds;                   // kTile x ks: a K chunk, then a V chunk
-    float *qs = lds + kTile * ks;      // rep x d_k: the group's rotated q heads
-    float *nk = qs + a.rep * a.d_k;    // PREP: the new k and v rows (2 x d_k)
-    const int nt = blockDim.x;
+    const int dk = FULL ? 64 * DKL : a.d_k;
+    // o[j] of a lane holds value dof(j): d = 2 lane + j (PAIRED: one 8-byte
+    // LDS read per position) or d = lane + 64 j
+    constexpr bool PAIRED = FULL && DKL == 2;
+    const int nh = a.rep > 4 ? a.rep : 4;  // waves per tile group
+    const int ng = 64 * nh;                // threads per tile group
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave / nh;
+    const int r = wave - grp * nh;  // this wave's q head in the kv group
+    const int tg = tid - grp * ng;  // thread index within the group
+    const bool head = r < a.rep;
+    auto dof = [&](int j) { return PAIRED ? 2 * lane + j : lane + 64 * j; };
+    float *kt = lds + (size_t)grp * kTile * ks;  // kTile x ks: a K chunk, then a V chunk
+    float *qs = lds + (size_t)a.tw * kTile * ks; // rep x d_k: the kv group's rotated q heads
+    float *nk = qs + a.rep * dk;                 // PREP: the new k and v rows (2 x d_k)
+    float *mg = nk + 2 * dk;                     // rep x tw x (d_k + 2): the groups' states
+    float *ew = mg + (size_t)a.rep * a.tw * (dk + 2) + (size_t)wave * kTile;  // this wave's tile weights
     const int split = blockIdx.x;
     const int qi = blockIdx.y / a.n_kv, g = blockIdx.y - qi * a.n_kv;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int r = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's q head in the group
-    const bool head = r < a.rep;
-    const int dk = a.d_k;
     const int limit = a.cache_len + qi + 1;
-    const int p0 = split * a.tps * kTile;
+    const int w0 = split * a.tw * a.tps * kTile;  // the workgroup's range [w0, w1)
+    const int w1 = min(w0 + a.tw * a.tps * kTile, limit);
+    const int p0 = w0 + grp * a.tps * kTile;      // this group's range [p0, p1) (may be empty)
     const int p1 = min(p0 + a.tps * kTile, limit);
     // rows read from the cache: PREP builds the new one (position cache_len) itself
     const int have = PREP ? a.cache_len : limit;
-    const bool owns_new = PREP && a.cache_len >= p0 && a.cache_len < p1;
+    const bool owns_new = PREP && a.cache_len >= w0 && a.cache_len < w1;
     const float *kb = a.cache_k + (size_t)g * a.cap * dk;
     const float *vb = a.cache_v + (size_t)g * a.cap * dk;
     constexpr bool one_chunk = DKL <= 2;  // d_k <= kChunk
 
     v4f kreg[8], vreg[8];
     auto load_chunk = [&](int t0, int n, int c0, bool k_too, bool v_too) {
-        const int q4 = min(kChunk, dk - c0) / 4;
+        const int q4 = FULL ? 16 * DKL : min(kChunk, dk - c0) / 4;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int i = tid + nt * u;
+            const int i = tg + ng * u;
             if (i < n * q4) {
-                const int p = i / q4, c = (i - p * q4) * 4;
+                const int p = (int)((unsigned)i / (unsigned)q4), c = (i - p * q4) * 4;
                 if (t0 + p < have) {
-                    const size_t at = (size_t)(t0 + p) * dk + c0 + c;
-                    if (k_too) kreg[u] = *(const v4f *)(kb + at);
-                    if (v_too) vreg[u] = *(const v4f *)(vb + at);
+                    // 32-bit byte offset from the head's base (SGPR base + VGPR offset)
+                    const uint32_t at = ((uint32_t)(t0 + p) * (uint32_t)dk + (uint32_t)(c0 + c)) * 4u;
+                    if (k_too) kreg[u] = *(const v4f *)((const char *)kb + at);
+                    if (v_too) vreg[u] = *(const v4f *)((const char *)vb + at);
                 }
             }
         }
     };
+    // rows n .. n rounded up to 8 are written as zeros (the value loop reads
+    // whole groups of eight rows)
     auto store_chunk = [&](const v4f *reg, int n, int c0, int newp, const float *newrow) {
-        const int q4 = min(kChunk, dk - c0) / 4;
+        const int q4 = FULL ? 16 * DKL : min(kChunk, dk - c0) / 4;
+        const int n8 = (n + 7) & ~7;
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            const int i = tid + nt * u;
-            if (i < n * q4) {
-                const int p = i / q4, c = (i - p * q4) * 4;
-                *(v4f *)(kt + p * ks + c) = (p == newp) ? *(const v4f *)(newrow + c0 + c) : reg[u];
+            const int i = tg + ng * u;
+            if (i < n8 * q4) {
+                const int p = (int)((unsigned)i / (unsigned)q4), c = (i - p * q4) * 4;
+                const v4f z = {0.0f, 0.0f, 0.0f, 0.0f};
+                *(v4f *)(kt + p * ks + c) = p >= n ? z : ((p == newp) ? *(const v4f *)(newrow + c0 + c) : reg[u]);
             }
         }
     };
-    // the first tile's K (and V) rows: issued before anything waits
-    if (p0 < p1) load_chunk(p0, min(kTile, p1 - p0), 0, true, one_chunk);
+    // the first tile's K rows (FULL: and V rows) are issued before anything
+    // waits; otherwise its V rows after the q preparation, whose registers
+    // they would share
+    if (p0 < p1) load_chunk(p0, min(kTile, p1 - p0), 0, true, FULL && one_chunk);
 
     if (PREP) {
         const int pos = a.start_pos + qi;
-        if (head) {
+        if (head && grp == 0) {
             const int h = g * a.rep + r;
             prep_row(qs + r * dk, a.q + (size_t)qi * a.n_heads * dk + (size_t)h * dk, dk, a.q_bias, h * dk, a.qb_len,
                      a.q_norm, a.eps, a.freqs, a.half_dim, pos, lane);
         }
-        if (owns_new && r == (nt >> 6) - 1) {  // the last wave: no q head unless rep fills the workgroup
+        // the workgroup's last wave: no q head to build unless there is one group
+        // and rep fills it
+        if (owns_new && wave == (int)(blockDim.x >> 6) - 1) {
             const size_t off = (size_t)qi * a.n_kv * dk + (size_t)g * dk;
             prep_row(nk, a.k + off, dk, a.k_bias, g * dk, a.kb_len, a.k_norm, a.eps, a.freqs, a.half_dim, pos, lane);
             const size_t at = ((size_t)g * a.cap + (size_t)a.cache_len) * dk;
@@ -204,38 +238,41 @@ __global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
             }
         }
     } else {
-        const float4 *qg = (const float4 *)(a.qrot + ((size_t)qi * a.n_heads + (size_t)g * a.rep) * dk);
-        for (int i = tid; i < a.rep * dk / 4; i += nt) ((float4 *)qs)[i] = qg[i];
+        const float4 *qq = (const float4 *)(a.qrot + ((size_t)qi * a.n_heads + (size_t)g * a.rep) * dk);
+        for (int i = tid; i < a.rep * dk / 4; i += (int)blockDim.x) ((float4 *)qs)[i] = qq[i];
     }
+
+    if (!FULL && one_chunk && p0 < p1) load_chunk(p0, min(kTile, p1 - p0), 0, false, true);
 
     float m = -INFINITY, l = 0.0f, o[DKL];
 #pragma unroll
     for (int j = 0; j < DKL; j++) o[j] = 0.0f;
-    for (int t0 = p0; t0 < p1; t0 += kTile) {
-        const int n = min(kTile, p1 - t0);  // valid positions of this tile (lanes < n)
+    for (int it = 0; it < a.tps; it++) {
+        const int t0 = p0 + it * kTile;
+        const int n = max(0, min(kTile, p1 - t0));  // valid positions of this tile (lanes < n)
         const int newp = owns_new ? a.cache_len - t0 : -1;  // row of the new position in this tile
         float dot = 0.0f;
         for (int c0 = 0; c0 < dk; c0 += kChunk) {
             const int cw = min(kChunk, dk - c0);
-            if (t0 != p0 || c0 != 0) load_chunk(t0, n, c0, true, one_chunk);
+            if (it != 0 || c0 != 0) load_chunk(t0, n, c0, true, one_chunk);
             __syncthreads();  // the previous users of kt are done (and qs / nk are written)
             store_chunk(kreg, n, c0, newp, nk);
             __syncthreads();
             if (head && lane < n) {
                 const float *qr = qs + r * dk + c0;
                 const float *kr = kt + lane * ks;
-                for (int d0 = 0; d0 < cw; d0 += 32) {
-                    // eight 4-element steps: their LDS reads issue together, the
-                    // products are added one by one in element order
-                    v4f kv[8], qv[8];
+                for (int d0 = 0; d0 < cw; d0 += 4 * kDotSteps) {
+                    // kDotSteps 4-element steps: their LDS reads issue together,
+                    // the products are added one by one in element order
+                    v4f kv[kDotSteps], qv[kDotSteps];
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
+                    for (int u = 0; u < kDotSteps; u++) {
                         kv[u] = *(const v4f *)(kr + d0 + 4 * u);
                         qv[u] = *(const v4f *)(qr + d0 + 4 * u);
                     }
-                    const int steps = min(8, (cw - d0) / 4);
+                    const int steps = min(kDotSteps, (cw - d0) / 4);
 #pragma unroll
-                    for (int u = 0; u < 8; u++) {
+                    for (int u = 0; u < kDotSteps; u++) {
                         if (u < steps) {
                             dot += qv[u].x * kv[u].x;
                             dot += qv[u].y * kv[u].y;
@@ -246,9 +283,9 @@ __global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
                 }
             }
         }
-        // online softmax of this tile
+        // online softmax of this tile (a tile without positions changes nothing)
         float e = 0.0f;
-        if (head) {
+        if (head && n > 0) {
             const float sc = lane < n ? dot * a.scale : -INFINITY;
             float mt = sc;
 #pragma unroll
@@ -269,27 +306,44 @@ __global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
             store_chunk(vreg, n, c0, newp, nk + dk);
             __syncthreads();
             if (head) {
+                // the weights go through LDS: eight per group of positions in two
+                // broadcast reads (0 past the tile's end, where the rows are zeros)
+                if (c0 == 0) {
+                    ew[lane] = e;
+                    wave_lds_sync();
+                }
                 for (int q0 = 0; q0 < n; q0 += 8) {
-                    // eight positions' values read together, then added in order
-                    float vv[8][DKL];
+                    const v4f ea = *(const v4f *)(ew + q0), eb = *(const v4f *)(ew + q0 + 4);
+                    const float ev[8] = {ea.x, ea.y, ea.z, ea.w, eb.x, eb.y, eb.z, eb.w};
+                    if (PAIRED) {
+                        // eight positions' values read together, then accumulated in
+                        // order (fused multiply-add: one rounding per step)
+                        v2f vv[8];
 #pragma unroll
-                    for (int pp = 0; pp < 8; pp++) {
-                        const float *vr = kt + (q0 + pp) * ks - c0;
+                        for (int pp = 0; pp < 8; pp++) vv[pp] = *(const v2f *)(kt + (q0 + pp) * ks + 2 * lane);
 #pragma unroll
-                        for (int j = 0; j < DKL; j++) {
-                            const int d = lane + 64 * j;
-                            // rows past the tile's end hold stale LDS data: zero, not
-                            // a zero weight times whatever is there (NaN * 0 is NaN)
-                            vv[pp][j] = (q0 + pp < n && d >= c0 && d < c0 + cw) ? vr[d] : 0.0f;
+                        for (int pp = 0; pp < 8; pp++) {
+                            o[0] = __builtin_fmaf(ev[pp], vv[pp].x, o[0]);
+                            o[PAIRED ? 1 : 0] = __builtin_fmaf(ev[pp], vv[pp].y, o[PAIRED ? 1 : 0]);
                         }
-                    }
+                    } else {
+                        float vv[8][DKL];
 #pragma unroll
-                    for (int pp = 0; pp < 8; pp++) {
-                        const float ep = lane_bcast(e, q0 + pp);  // 0 past the tile's end
+                        for (int pp = 0; pp < 8; pp++) {
+                            const float *vr = kt + (q0 + pp) * ks - c0;
 #pragma unroll
-                        for (int j = 0; j < DKL; j++) {
-                            const int d = lane + 64 * j;
-                            if (d >= c0 && d < c0 + cw) o[j] = o[j] + ep * vv[pp][j];
+                            for (int j = 0; j < DKL; j++) {
+                                const int d = dof(j);
+                                vv[pp][j] = (d >= c0 && d < c0 + cw) ? vr[d] : 0.0f;
+                            }
+                        }
+#pragma unroll
+                        for (int pp = 0; pp < 8; pp++) {
+#pragma unroll
+                            for (int j = 0; j < DKL; j++) {
+                                const int d = dof(j);
+                                if (d >= c0 && d < c0 + cw) o[j] = __builtin_fmaf(ev[pp], vv[pp][j], o[j]);
+                            }
                         }
                     }
                 }
@@ -297,19 +351,65 @@ __global__ void __launch_bounds__(512) attn_split_kernel(AttnArgs a) {
         }
     }
 
-    // this split's partial of the head: running max, sum, weighted values
+    // the groups' states meet in LDS; group 0 merges them (M = max, weights
+    // w_t = float32(exp(float64(m_t - M))), L = wave_sum over lanes t of
+    // l_t * w_t, O = sum over t in order of o_t * w_t), as attn_combine_kernel does
+    const int sst = dk + 2;
     if (head) {
-        const size_t stride = (size_t)dk + 2;
-        const int h = g * a.rep + r;
-        float *pp = a.part + (((size_t)qi * a.n_heads + h) * a.splits + split) * stride;
+        float *st = mg + ((size_t)r * a.tw + grp) * sst;
         if (lane == 0) {
-            pp[0] = m;
-            pp[1] = l;
+            st[0] = m;
+            st[1] = l;
         }
 #pragma unroll
         for (int j = 0; j < DKL; j++) {
-            const int d = lane + 64 * j;
-            if (d < dk) pp[2 + d] = o[j];
+            const int d = dof(j);
+            if (d < dk) st[2 + d] = o[j];
+        }
+    }
+    __syncthreads();
+    if (!head || grp != 0) return;
+    const float *sb = mg + (size_t)r * a.tw * sst;
+    float M = -INFINITY;
+    for (int t = 0; t < a.tw; t++) M = fmaxf(M, sb[t * sst]);
+    const bool mine = lane < a.tw;
+    const float ml = mine ? sb[lane * sst] : -INFINITY;
+    const float ll = mine ? sb[lane * sst + 1] : 0.0f;
+    // a group without positions weighs 0 (also when no group has any: a split
+    // of a causal row can lie wholly past it, and then leaves (-inf, 0, 0))
+    const float wl = (mine && ml != -INFINITY) ? (float)exp((double)(ml - M)) : 0.0f;
+    const float L = wave_sum(0.0f + ll * wl);
+    float O[DKL];
+#pragma unroll
+    for (int j = 0; j < DKL; j++) O[j] = 0.0f;
+    for (int t = 0; t < a.tw; t++) {
+        const float w = lane_bcast(wl, t);
+#pragma unroll
+        for (int j = 0; j < DKL; j++) {
+            const int d = dof(j);
+            O[j] = O[j] + (d < dk ? sb[t * sst + 2 + d] : 0.0f) * w;
+        }
+    }
+    const int h = g * a.rep + r;
+    if (a.splits == 1) {
+        const float inv = 1.0f / L;
+        float *dst = a.out + ((size_t)qi * a.n_heads + h) * dk;  // mergeHeadsDataF32 layout
+#pragma unroll
+        for (int j = 0; j < DKL; j++) {
+            const int d = dof(j);
+            if (d < dk) dst[d] = O[j] * inv;
+        }
+    } else {
+        // this split's partial of the head: running max, sum, weighted values
+        float *pp = a.part + (((size_t)qi * a.n_heads + h) * a.splits + split) * sst;
+        if (lane == 0) {
+            pp[0] = M;
+            pp[1] = L;
+        }
+#pragma unroll
+        for (int j = 0; j < DKL; j++) {
+            const int d = dof(j);
+            if (d < dk) pp[2 + d] = O[j];
         }
     }
 }
@@ -371,35 +471,82 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 
 }  // namespace
 
-void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps,
+namespace {
+size_t attn_lds_bytes(int tw, int rep, int d_k) {
+    const int nh = rep > 4 ? rep : 4;
+    return ((size_t)tw * kTile * (kChunk + 4) + (size_t)(rep + 2) * d_k + (size_t)tw * rep * (d_k + 2) +
+            (size_t)tw * nh * kTile) *
+           sizeof(float);
+}
+// the device's LDS per workgroup (read once)
+size_t lds_per_block() {
+    static const size_t v = [] {
+        int dev = 0, b = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&b, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || b <= 0)
+            return (size_t)64 * 1024;
+        return (size_t)b;
+    }();
+    return v;
+}
+}  // namespace
+
+void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw,
                     size_t *ws_bytes) {
     const int tiles = (kv_len + kTile - 1) / kTile;
     const int pairs = seq * n_kv;
-    const int target = tuning().attn_target_blocks;
-    int S = (target + pairs - 1) / pairs;
-    S = S < 1 ? 1 : (S > tiles ? tiles : S);
-    const int t = (tiles + S - 1) / S;
-    S = (tiles + t - 1) / t;
+    const int rep = n_heads / n_kv, nh = rep > 4 ? rep : 4;
+    const Tuning &T = tuning();
+    // tile groups per workgroup: at most kMaxWaves waves, and what LDS holds
+    int G = kMaxWaves / nh;
+    G = G < T.attn_tile_groups ? G : T.attn_tile_groups;
+    G = G < tiles ? G : tiles;
+    while (G > 1 && attn_lds_bytes(G, rep, d_k) > lds_per_block()) G--;
+    G = G < 1 ? 1 : G;
+    int S, t;
+    if (tiles <= G) {
+        // one workgroup per (row, kv head), a tile per group: no combine launch
+        S = 1;
+        t = 1;
+        G = tiles;
+    } else {
+        // splits of at most two groups (waves that share a SIMD share its
+        // VALU), about attn_target_blocks workgroups over the (row, kv head)
+        // pairs; more tiles per group only past that
+        G = G < 2 ? G : 2;
+        S = (T.attn_target_blocks + pairs - 1) / pairs;
+        const int smax = (tiles + G - 1) / G;
+        S = S < 1 ? 1 : (S > smax ? smax : S);
+        t = (tiles + S * G - 1) / (S * G);
+        S = (tiles + t * G - 1) / (t * G);
+    }
     *splits = S;
     *tps = t;
+    *tw = G;
     const size_t qrot = (size_t)seq * n_heads * d_k * sizeof(float);
-    const size_t part = (size_t)seq * n_heads * S * (d_k + 2) * sizeof(float);
+    const size_t part = S > 1 ? (size_t)seq * n_heads * S * (d_k + 2) * sizeof(float) : 0;
     *ws_bytes = ((qrot + 255) & ~(size_t)255) + part;
 }
 
 template <bool PREP>
 void launch_split(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t s) {
-    const dim3 block(64 * (a.rep > 4 ? a.rep : 4));
+    const dim3 block(64 * (a.rep > 4 ? a.rep : 4) * a.tw);
     switch ((a.d_k + 63) / 64) {
-    case 1: hipLaunchKernelGGL((attn_split_kernel<PREP, 1>), grid, block, lds, s, a); break;
-    case 2: hipLaunchKernelGGL((attn_split_kernel<PREP, 2>), grid, block, lds, s, a); break;
-    case 3: hipLaunchKernelGGL((attn_split_kernel<PREP, 3>), grid, block, lds, s, a); break;
-    default: hipLaunchKernelGGL((attn_split_kernel<PREP, 4>), grid, block, lds, s, a); break;
+    case 1:
+        if (a.d_k == 64) hipLaunchKernelGGL((attn_split_kernel<PREP, 1, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<PREP, 1, false>), grid, block, lds, s, a);
+        break;
+    case 2:
+        if (a.d_k == 128) hipLaunchKernelGGL((attn_split_kernel<PREP, 2, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((attn_split_kernel<PREP, 2, false>), grid, block, lds, s, a);
+        break;
+    case 3: hipLaunchKernelGGL((attn_split_kernel<PREP, 3, false>), grid, block, lds, s, a); break;
+    default: hipLaunchKernelGGL((attn_split_kernel<PREP, 4, false>), grid, block, lds, s, a); break;
     }
 }
 
 sllm_status launch_attention(const AttnArgs &a, hipStream_t s) {
-    const size_t lds = ((size_t)kTile * (kChunk + 4) + (size_t)(a.rep + 2) * a.d_k) * sizeof(float);
+    const size_t lds = attn_lds_bytes(a.tw, a.rep, a.d_k);
     if (a.seq == 1) {
         launch_split<true>(a, dim3(a.splits, a.n_kv), lds, s);
     } else {
@@ -408,8 +555,10 @@ sllm_status launch_attention(const AttnArgs &a, hipStream_t s) {
         launch_split<false>(a, dim3(a.splits, a.seq * a.n_kv), lds, s);
     }
     SLLM_HIP(hipGetLastError());
-    hipLaunchKernelGGL(attn_combine_kernel, dim3((a.seq * a.n_heads + 3) / 4), dim3(256), 0, s, a);
-    SLLM_HIP(hipGetLastError());
+    if (a.splits > 1) {
+        hipLaunchKernelGGL(attn_combine_kernel, dim3((a.seq * a.n_heads + 3) / 4), dim3(256), 0, s, a);
+        SLLM_HIP(hipGetLastError());
+    }
     return SLLM_OK;
 }
 

@@ -9,6 +9,7 @@ What must agree and how closely:
   vs the C library's), so within 4 ulp-of-|x| per element;
 * the attention output: the scores are the reference's sequential float32
   dots, the softmax sums and the weighted sum of values are reassociated
+  (the weighted sum with fused multiply-adds: one rounding per step)
   (split over positions and combined). Bound per output element, from the
   float64 scores s_k and weights p_k the oracle's rotated q and the cache
   give: sum_k p_k |v_k| (2 ds_k + (2 kv_len + 160) u + 6 u (max s - s_k)),
@@ -150,6 +151,24 @@ def test_decode_llama_heads(cache_len):
     rng = np.random.default_rng(cache_len)
     m = Model(8, 2, 128, 64, rng, base=500000.0)
     run_case(m, 1, cache_len, rng)
+
+
+@pytest.mark.parametrize("groups,target", [(1, 512), (2, 512), (4, 512), (4, 8), (3, 1)])
+@pytest.mark.parametrize("cache_len", [0, 63, 130, 300, 1100])
+def test_tile_groups_and_splits(groups, target, cache_len):
+    # 1-4 tile groups per workgroup, merged in LDS; one split (the workgroup
+    # writes the output) or several (the combine launch), including groups
+    # whose tiles lie past the causal range
+    sq.set_param("attn_tile_groups", groups)
+    sq.set_param("attn_target_blocks", target)
+    try:
+        rng = np.random.default_rng(cache_len + 1000 * groups)
+        m = Model(8, 2, 128, 64, rng, base=500000.0)
+        run_case(m, 1, cache_len, rng)
+        run_case(m, 3, cache_len, rng)
+    finally:
+        sq.set_param("attn_tile_groups", 4)
+        sq.set_param("attn_target_blocks", 512)
 
 
 def test_first_position_after_a_launch_that_leaves_nan_in_lds():
