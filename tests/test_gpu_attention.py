@@ -9,8 +9,8 @@ What must agree and how closely:
   vs the C library's), so within 4 ulp-of-|x| per element;
 * the attention output: the scores are the reference's sequential float32
   dots, the softmax sums and the weighted sum of values are reassociated
-  (the weighted sum with fused multiply-adds: one rounding per step)
-  (split over positions and combined). Bound per output element, from the
+  (split over positions and combined; the weighted sum with fused
+  multiply-adds, one rounding per step). Bound per output element, from the
   float64 scores s_k and weights p_k the oracle's rotated q and the cache
   give: sum_k p_k |v_k| (2 ds_k + (2 kv_len + 160) u + 6 u (max s - s_k)),
   u = 2^-24, ds_k = 4 u scale sum_d |q_d k_kd| (rotated inputs that differ in
