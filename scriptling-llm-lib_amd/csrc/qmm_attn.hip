@@ -427,11 +427,16 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     const float *pb = a.part + (size_t)pair * a.splits * stride;
     // splits in groups of 16: lane t holds m_t and l_t of its group, every
     // lane the values of its d for the whole group - all loaded together
-    // (a group's missing splits weigh 0 and add exact zeros)
+    // (a group's missing splits weigh 0 and add exact zeros). With at most 16
+    // splits the maximum comes from the same loads (one memory round);
+    // otherwise from a first pass over the maxima.
+    const bool one = a.splits <= 16;
     float M = -INFINITY;
-    for (int t = lane; t < a.splits; t += 64) M = fmaxf(M, pb[t * stride]);
+    if (!one) {
+        for (int t = lane; t < a.splits; t += 64) M = fmaxf(M, pb[t * stride]);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    }
     float Lp = 0.0f;
     float O[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int t0 = 0; t0 < a.splits; t0 += 16) {
@@ -450,7 +455,13 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
                 ov[u][jj] = (u < nt && d < dk) ? ob[d] : 0.0f;
             }
         }
-        const float wl = mine ? (float)exp((double)(ml - M)) : 0.0f;
+        if (one) {
+            M = ml;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+        }
+        // a split without positions (-inf) weighs 0
+        const float wl = (mine && ml != -INFINITY) ? (float)exp((double)(ml - M)) : 0.0f;
         Lp = Lp + ll * wl;
 #pragma unroll
         for (int u = 0; u < 16; u++) {
