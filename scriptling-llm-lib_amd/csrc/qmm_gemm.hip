@@ -53,7 +53,7 @@ struct alignas(16) Stage {
     int8_t a[kBM * kARow];                       // activation codes
     int8_t b[BN * brow_bytes<FMT>()];            // weight codes
     float xs[kKB][kBM];                          // activation scales
-    int sx[kKB][kBM];                            // Σxq
+    int sx[kKB][kBM];                            // Σxq (Q4_1 / Q5K1: float(Σxq), exact, as bits)
     uint16_t d[kKB][BN];                         // weight scales
     uint16_t m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? kKB : 1][BN];
     uint16_t dh[FMT == SLLM_Q5K1 ? kKB : 1][BN];
@@ -167,7 +167,8 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FM
         if (F::S_N % T == 0 || e < F::S_N) {
             const int blk = e / kBM, r = e % kBM;
             S.xs[blk][r] = f.xs[i];
-            S.sx[blk][r] = f.sx[i];
+            // the float form is converted once here instead of per output
+            S.sx[blk][r] = (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? __float_as_int((float)f.sx[i]) : f.sx[i];
         }
     }
 #pragma unroll
@@ -296,7 +297,7 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
                         } else {
                             // q41q8_row_amd64.s:65-71
                             const float t1 = (float)d[r] * wd;
-                            const float t2 = (float)sv[r] * wmn;
+                            const float t2 = __int_as_float(sv[r]) * wmn;
                             float tt = t1 + t2;
                             tt = tt * xv[r];
                             acc[i][j][r] = acc[i][j][r] + tt;
@@ -307,7 +308,7 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
 #pragma unroll
                         for (int r = 0; r < 4; r++) {
                             const float h1 = (float)h[r] * wdh;
-                            const float h2 = (float)sv[r] * 0.0f;
+                            const float h2 = __int_as_float(sv[r]) * 0.0f;
                             float hh = h1 + h2;
                             hh = hh * xv[r];
                             acc2[DUAL ? i : 0][DUAL ? j : 0][r] = acc2[DUAL ? i : 0][DUAL ? j : 0][r] + hh;
