@@ -231,7 +231,8 @@ sllm_status sllm_matmul_add_dev(const sllm_weight *w, const float *x_dev, int x_
  * (InferenceModelF32.KVCaches, initKVCaches model_f32.go:310-318; the
  * reference appends without bound, MaxSeqLen caps the context,
  * model_f32.go:599-602). Layout: layer-major, then head, position, d_k
- * (fp32, as the reference keeps it). d_k: a multiple of 4, at most 256.
+ * (fp32, as the reference keeps it). d_k: a multiple of 4, at most 256;
+ * max_seq x d_k x 4 bytes (one kv head of one layer) below 4 GiB.
  */
 typedef struct sllm_kv_cache sllm_kv_cache;
 sllm_status sllm_kv_cache_create(int n_layers, int n_kv_heads, int d_k, int max_seq, sllm_kv_cache **out);

@@ -925,6 +925,9 @@ sllm_status sllm_kv_cache_create(int n_layers, int n_kv_heads, int d_k, int max_
     if (n_layers <= 0 || n_kv_heads <= 0 || max_seq <= 0 || d_k <= 0)
         return set_error(SLLM_ERR_ARG, "KV cache dimensions must be positive");
     if (d_k % 4 != 0 || d_k > 256) return set_error(SLLM_ERR_SHAPE, "d_k must be a multiple of 4, at most 256");
+    // the attention kernels address one kv head's rows with 32-bit byte offsets
+    if ((int64_t)max_seq * d_k * (int64_t)sizeof(float) >= ((int64_t)1 << 32))
+        return set_error(SLLM_ERR_SHAPE, "max_seq x d_k x 4 bytes must stay below 4 GiB per kv head");
     sllm_status st = ensure_init();
     if (st != SLLM_OK) return st;
     auto *kv = new sllm_kv_cache();

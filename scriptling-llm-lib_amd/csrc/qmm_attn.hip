@@ -125,23 +125,23 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
 // - running max))), rescaled by the same form when the running max grows.
 //
 // The split is a.tw tile groups of nh = max(4, rep) waves (at most
-// kMaxWaves waves in all); group t takes
-// a.tps consecutive tiles of the split's range (every group runs the same
-// number of steps, so the workgroup barriers line up; a tile past the range
-// has no positions). Wave r of a group owns q head r; lane l holds the
-// values d = l + 64 j, j < DKL (DKL = d_k / 64 rounded up; FULL: d_k is
-// exactly 64 DKL, one K chunk). PREP (one query
-// row): group 0's waves first build the q heads (bias, norm, RoPE) in LDS,
-// and in the workgroup whose range holds the new position the last wave
-// builds the new k / v row, appends it to the cache and the groups use it
-// from LDS; otherwise attn_prep_kernel has done both. Per tile the K and V
-// rows are loaded together (K straight to LDS, V to registers while the
-// scores are computed, then to the same LDS buffer): one memory latency per
-// tile, overlapped with the q preparation for the first (whose V rows are
-// issued after that preparation). LDS reads are
-// issued in groups. At the end each wave leaves its (max, sum,
-// values) state in LDS and group 0 merges the groups' states in group order
-// exactly as attn_combine_kernel merges splits.
+// kMaxWaves waves in all); group t takes a.tps consecutive tiles of the
+// split's range (every group runs the same number of steps, so the
+// workgroup barriers line up; a tile past the range has no positions). Wave
+// r of a group owns q head r and keeps the value sums of d_k / 64 (rounded
+// up) dimensions per lane: d = 2 lane + j when d_k is 128 (one 8-byte LDS
+// read per position), d = lane + 64 j otherwise. FULL: d_k is exactly 64 DKL.
+// PREP (one query row): group 0's waves first build the q heads (bias, norm,
+// RoPE) in LDS, and in the workgroup whose range holds the new position the
+// last wave builds the new k / v row, appends it to the cache and the groups
+// use it from LDS; otherwise attn_prep_kernel has done both. Per tile the K
+// and V rows are loaded together (K straight to LDS, V to registers while
+// the scores are computed, then to the same LDS buffer): one memory latency
+// per tile, overlapped with the q preparation for the first tile (FULL; the
+// other head sizes issue its V rows after the preparation, whose registers
+// they would share). LDS reads are issued in groups. At the end each wave
+// leaves its (max, sum, values) state in LDS and group 0 merges the groups'
+// states in group order exactly as attn_combine_kernel merges splits.
 template <bool PREP, int DKL, bool FULL>
 __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) {
 

@@ -64,6 +64,7 @@ def test_argument_errors_need_no_device():
     assert lib.sllm_kv_cache_create(0, 8, 128, 16, C.byref(kv)) == 1                      # no layers
     assert lib.sllm_kv_cache_create(2, 8, 130, 16, C.byref(kv)) == 3                      # d_k % 4
     assert lib.sllm_kv_cache_create(2, 8, 512, 16, C.byref(kv)) == 3                      # d_k > 256
+    assert lib.sllm_kv_cache_create(1, 1, 256, 1 << 22, C.byref(kv)) == 3                  # 4 GiB per kv head
     assert lib.sllm_kv_cache_length(None, 0, C.byref(C.c_int())) == 1
     assert lib.sllm_kv_cache_set_length(None, 0) == 1
     prm = sq.AttnParams(n_heads=32, n_kv_heads=8, d_k=128, rope_half_dim=64)
