@@ -199,6 +199,9 @@ int parse_qtype(const char *q) {
 }
 
 sllm_status alloc_weight(int fmt, int rows, int cols, sllm_weight **out, int layout = -1) {
+    // the GEMV addresses a plane with 32-bit byte offsets (16-byte entries at most)
+    if ((int64_t)rows * (cols / 32) >= ((int64_t)1 << 28))
+        return set_error(SLLM_ERR_SHAPE, "weight too large: at most 2^28 blocks of 32 weights");
     auto *w = new sllm_weight();
     w->fmt = fmt;
     w->layout = layout < 0 ? fmt : layout;
