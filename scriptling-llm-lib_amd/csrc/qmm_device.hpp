@@ -224,14 +224,14 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
         float4 b = xb[jj + 4];  // elements 16+4jj ..
         const float av[4] = {a.x, a.y, a.z, a.w};
         const float bv[4] = {b.x, b.y, b.z, b.w};
+        // the four codes of elements 4jj+k (lo) and 16+4jj+k (hi) as bytes k,
+        // so each converts with one byte-to-float instruction
+        const uint32_t lo = (w[jj] & 0x0f0f0f0fu) | ((uint32_t)spread4(qh >> (4 * jj)) << 4);
+        const uint32_t hi = ((w[jj] >> 4) & 0x0f0f0f0fu) | ((uint32_t)spread4(qh >> (16 + 4 * jj)) << 4);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            int j = 4 * jj + k;
-            uint32_t byte = (w[jj] >> (8 * k)) & 0xffu;
-            int q0 = (int)((byte & 0x0fu) | (((qh >> j) & 1u) << 4));
-            int q1 = (int)((byte >> 4) | (((qh >> (j + 16)) & 1u) << 4));
-            float v0 = (float)q0 - 16.0f;
-            float v1 = (float)q1 - 16.0f;
+            float v0 = (float)((lo >> (8 * k)) & 0xffu) - 16.0f;
+            float v1 = (float)((hi >> (8 * k)) & 0xffu) - 16.0f;
             float p0 = v0 * av[k];
             float p1 = v1 * bv[k];
             float pair = p0 + p1;

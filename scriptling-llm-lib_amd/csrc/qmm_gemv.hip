@@ -104,7 +104,9 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     // so that it overlaps its loads with its compute instead of issuing
     // everything at once and doing all its compute after the last byte lands.
     const int lg = (G + 63) / 64;
-    const int nb_cap = T.gemv_max_nb;
+    // Q5_0 reads 32 fp32 activations per block from LDS: more than two blocks
+    // per lane per unit only adds registers (measured: 3 % slower at NB 7)
+    const int nb_cap = fmt == SLLM_Q5_0 && T.gemv_max_nb > 2 ? 2 : T.gemv_max_nb;
     int NB = lg;
     if (lg > nb_cap) {
         NB = nb_cap;
