@@ -37,14 +37,16 @@ constexpr int kBM = 64;   // activation rows per workgroup
 constexpr int kKB = 4;    // blocks (x 32 elements) per K stage
 constexpr int kARow = kKB * 32 + 8;  // LDS bytes per activation row (padded: conflict-free b64 reads)
 
-// Bytes of weight codes per block in LDS, per format.
+// Bytes of weight codes per block in HBM, per format; in LDS every format
+// holds 32 one-byte codes per block (Q4 nibbles are expanded when a stage is
+// stored, once per workgroup instead of once per wave that reads them).
 template <int FMT>
 constexpr int wcode_bytes() {
     return FMT == SLLM_Q8_0 ? 32 : 16;
 }
 template <int FMT>
 constexpr int brow_bytes() {
-    return kKB * wcode_bytes<FMT>() + 8;  // padded
+    return kKB * 32 + 8;  // padded
 }
 
 template <int FMT, int BN>
@@ -54,9 +56,11 @@ struct alignas(16) Stage {
     int8_t b[BN * brow_bytes<FMT>()];            // weight codes
     float xs[kKB][kBM];                          // activation scales
     int sx[kKB][kBM];                            // Σxq (Q4_1 / Q5K1: float(Σxq), exact, as bits)
-    uint16_t d[kKB][BN];                         // weight scales
-    uint16_t m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? kKB : 1][BN];
-    uint16_t dh[FMT == SLLM_Q5K1 ? kKB : 1][BN];
+    // weight scales and mins, decoded to fp32 once per workgroup (Q8_0: the
+    // reference's f16 table, the others exact)
+    float d[kKB][BN];
+    float m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? kKB : 1][BN];
+    float dh[FMT == SLLM_Q5K1 ? kKB : 1][BN];
     uint32_t hb[FMT == SLLM_Q5K1 ? kKB : 1][BN];
 };
 
@@ -156,9 +160,18 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FM
         if (F::B_N % T == 0 || e < F::B_N) {
             const int r = e / (kKB * WB), rem = e % (kKB * WB);
             const int blk = rem / WB, half = rem % WB;
-            int2 *p = (int2 *)(S.b + r * brow_bytes<FMT>() + blk * wcode_bytes<FMT>() + half * 16);
-            p[0] = make_int2(f.b[i].x, f.b[i].y);
-            p[1] = make_int2(f.b[i].z, f.b[i].w);
+            int2 *p = (int2 *)(S.b + r * brow_bytes<FMT>() + blk * 32 + half * 16);
+            if (FMT == SLLM_Q8_0) {
+                p[0] = make_int2(f.b[i].x, f.b[i].y);
+                p[1] = make_int2(f.b[i].z, f.b[i].w);
+            } else {
+                // byte j holds element j (low nibble) and j + 16 (high nibble)
+                const int lo = 0x0f0f0f0f;
+                p[0] = make_int2(f.b[i].x & lo, f.b[i].y & lo);
+                p[1] = make_int2(f.b[i].z & lo, f.b[i].w & lo);
+                p[2] = make_int2((f.b[i].x >> 4) & lo, (f.b[i].y >> 4) & lo);
+                p[3] = make_int2((f.b[i].z >> 4) & lo, (f.b[i].w >> 4) & lo);
+            }
         }
     }
 #pragma unroll
@@ -176,10 +189,11 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FM
         const int e = tid + T * i;
         if (F::W_N % T == 0 || e < F::W_N) {
             const int blk = e / BN, c = e % BN;
-            S.d[blk][c] = f.d[i];
-            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][c] = f.m[i];
+            S.d[blk][c] = (FMT == SLLM_Q8_0) ? f16_lut(f.d[i]) : f16_exact(f.d[i]);
+            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1)
+                S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][c] = f16_exact(f.m[i]);
             if (FMT == SLLM_Q5K1) {
-                S.dh[FMT == SLLM_Q5K1 ? blk : 0][c] = f.dh[i];
+                S.dh[FMT == SLLM_Q5K1 ? blk : 0][c] = f16_exact(f.dh[i]);
                 S.hb[FMT == SLLM_Q5K1 ? blk : 0][c] = f.hb[i];
             }
         }
@@ -189,11 +203,7 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FM
 // B operand from LDS: 8 codes (chunk c of the block) of weight row `row`.
 template <int FMT, int BN>
 __device__ __forceinline__ long b_frag(const Stage<FMT, BN> &S, int row, int blk, int c) {
-    const int8_t *base = S.b + row * brow_bytes<FMT>() + blk * wcode_bytes<FMT>();
-    if (FMT == SLLM_Q8_0) return *(const long *)(base + c * 8);
-    const long v = *(const long *)(base + (c & 1) * 8);
-    const long lo = 0x0f0f0f0f0f0f0f0fL;
-    return (c < 2) ? (v & lo) : ((v >> 4) & lo);
+    return *(const long *)(S.b + row * brow_bytes<FMT>() + blk * 32 + c * 8);
 }
 
 // Q5K1 high operand: elements 8c..8c+7 of the mask as 0/1 bytes.
@@ -268,12 +278,12 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
             for (int j = 0; j < 2; j++) {
                 const int col = wn * 32 + 16 * j + r16;
                 const long b = b_frag<FMT, BN>(S, col, blk, c4);
-                const float wd = (FMT == SLLM_Q8_0) ? f16_lut(S.d[blk][col]) : f16_exact(S.d[blk][col]);
+                const float wd = S.d[blk][col];
                 float wmn = 0.0f, wdh = 0.0f;
                 long bh = 0;
-                if (FMT == SLLM_Q4_1 || DUAL) wmn = f16_exact(S.m[(FMT == SLLM_Q4_1 || DUAL) ? blk : 0][col]);
+                if (FMT == SLLM_Q4_1 || DUAL) wmn = S.m[(FMT == SLLM_Q4_1 || DUAL) ? blk : 0][col];
                 if (DUAL) {
-                    wdh = f16_exact(S.dh[DUAL ? blk : 0][col]);
+                    wdh = S.dh[DUAL ? blk : 0][col];
                     bh = bits_frag(S.hb[DUAL ? blk : 0][col], c4);
                 }
 #pragma unroll
