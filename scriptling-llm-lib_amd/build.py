@@ -23,6 +23,11 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions. The GEMM's MFMA results feed VALU arithmetic directly:
+# keeping them in VGPRs (not AGPRs) saves a v_accvgpr_read per value.
+EXTRA_FLAGS = {"qmm_gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _run(cmd: list[str]) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
     # hipcc's host pass warns that it does not know the packed-fp32 feature: harmless.
@@ -42,7 +47,8 @@ def build(verbose: bool = False) -> str:
     srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
     objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in srcs]
     inc = ["-I", os.path.join(ROOT, "include"), "-I", CSRC]
-    cmds = [[hipcc, *HIPCC_FLAGS, *inc, "-c", os.path.join(CSRC, s), "-o", o] for s, o in zip(srcs, objs)]
+    cmds = [[hipcc, *HIPCC_FLAGS, *EXTRA_FLAGS.get(s, []), *inc, "-c", os.path.join(CSRC, s), "-o", o]
+            for s, o in zip(srcs, objs)]
     if verbose:
         for c in cmds:
             print(" ".join(c), flush=True)
