@@ -317,10 +317,13 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
                         const v4i h = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bh, z, 0, 0, 0);
 #pragma unroll
                         for (int r = 0; r < 4; r++) {
+                            // The reference's high pass adds float(Σxq) * (+0), a
+                            // signed zero (Σxq is finite): h1 + ±0 is h1 unless h1
+                            // is itself a zero, and a zero term leaves acc2 (which
+                            // starts at +0, so is never -0) unchanged whatever its
+                            // sign. Omitting that add gives the same acc2 bits.
                             const float h1 = (float)h[r] * wdh;
-                            const float h2 = __int_as_float(sv[r]) * 0.0f;
-                            float hh = h1 + h2;
-                            hh = hh * xv[r];
+                            const float hh = h1 * xv[r];
                             acc2[DUAL ? i : 0][DUAL ? j : 0][r] = acc2[DUAL ? i : 0][DUAL ? j : 0][r] + hh;
                         }
                     }
