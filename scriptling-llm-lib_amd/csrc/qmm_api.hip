@@ -417,6 +417,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemv_inflight_kb") && value >= 64) t.gemv_inflight_kb = value;
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "attn_tile_groups") && value >= 1 && value <= 4) t.attn_tile_groups = value;
+    else if (!std::strcmp(name, "attn_head_slices") && value >= 0 && value <= 64) t.attn_head_slices = value;
     else if (!std::strcmp(name, "gemm_wn") && (value == 0 || value == 1 || value == 2 || value == 4)) t.gemm_wn = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
@@ -1012,9 +1013,9 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     sllm_status st = ensure_init();
     if (st != SLLM_OK) return st;
     hipStream_t s = (hipStream_t)stream;
-    int splits = 0, tps = 0, tw = 0;
+    int splits = 0, tps = 0, tw = 0, hs = 1;
     size_t wsb = 0;
-    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &wsb);
+    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &hs, &wsb);
     void *ws = nullptr;
     size_t cap = 0;
     if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
@@ -1051,6 +1052,7 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
     a.splits = splits;
     a.tps = tps;
     a.tw = tw;
+    a.hs = hs;
     if ((st = launch_attention(a, s)) != SLLM_OK) return st;
     kv->len[(size_t)layer] = cl + seq_len;
     return SLLM_OK;

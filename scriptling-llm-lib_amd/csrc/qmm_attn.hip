@@ -127,10 +127,14 @@ __global__ void __launch_bounds__(64) attn_prep_kernel(AttnArgs a) {
 // The split is a.tw tile groups of nh = max(4, rep) waves (at most
 // kMaxWaves waves in all); group t takes a.tps consecutive tiles of the
 // split's range (every group runs the same number of steps, so the
-// workgroup barriers line up; a tile past the range has no positions). Wave
-// r of a group owns q head r and keeps the value sums of d_k / 64 (rounded
-// up) dimensions per lane: d = 2 lane + j when d_k is 128 (one 8-byte LDS
-// read per position), d = lane + 64 j otherwise. FULL: d_k is exactly 64 DKL.
+// workgroup barriers line up; a tile past the range has no positions). The
+// kv group's q heads are shared by a.hs workgroups (head slices) of hp =
+// rep / hs heads each; in group t, wave r owns slice head hr = (r - t hp)
+// mod nh if hr < hp (the owning waves of successive groups start on
+// successive SIMDs), and keeps the value sums of d_k / 64 (rounded up)
+// dimensions per lane: d = 2 lane + j when d_k is 128 (one 8-byte LDS read
+// per position), d = lane + 64 j otherwise. FULL: d_k is exactly 64 DKL.
+// Every head's arithmetic is the same whatever hs is.
 // PREP (one query row): group 0's waves first build the q heads (bias, norm,
 // RoPE) in LDS, and in the workgroup whose range holds the new position the
 // last wave builds the new k / v row, appends it to the cache and the groups
@@ -152,21 +156,25 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
     // LDS read per position) or d = lane + 64 j
     constexpr bool PAIRED = FULL && DKL == 2;
     const int nh = a.rep > 4 ? a.rep : 4;  // waves per tile group
+    const int hp = a.rep / a.hs;           // q heads per workgroup
     const int ng = 64 * nh;                // threads per tile group
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int grp = wave / nh;
-    const int r = wave - grp * nh;  // this wave's q head in the kv group
-    const int tg = tid - grp * ng;  // thread index within the group
-    const bool head = r < a.rep;
+    const int r = wave - grp * nh;
+    const int hr = (r + nh - (grp * hp) % nh) % nh;  // this wave's q head in the slice, if < hp
+    const int tg = tid - grp * ng;                   // thread index within the group
+    const bool head = hr < hp;
     auto dof = [&](int j) { return PAIRED ? 2 * lane + j : lane + 64 * j; };
     float *kt = lds + (size_t)grp * kTile * ks;  // kTile x ks: a K chunk, then a V chunk
-    float *qs = lds + (size_t)a.tw * kTile * ks; // rep x d_k: the kv group's rotated q heads
-    float *nk = qs + a.rep * dk;                 // PREP: the new k and v rows (2 x d_k)
-    float *mg = nk + 2 * dk;                     // rep x tw x (d_k + 2): the groups' states
-    float *ew = mg + (size_t)a.rep * a.tw * (dk + 2) + (size_t)wave * kTile;  // this wave's tile weights
+    float *qs = lds + (size_t)a.tw * kTile * ks; // hp x d_k: the slice's rotated q heads
+    float *nk = qs + hp * dk;                    // PREP: the new k and v rows (2 x d_k)
+    float *mg = nk + 2 * dk;                     // hp x tw x (d_k + 2): the groups' states
+    float *ew = mg + (size_t)hp * a.tw * (dk + 2) + (size_t)wave * kTile;  // this wave's tile weights
     const int split = blockIdx.x;
-    const int qi = blockIdx.y / a.n_kv, g = blockIdx.y - qi * a.n_kv;
+    const int ys = blockIdx.y / a.hs, sl = blockIdx.y - ys * a.hs;  // (row, kv head), head slice
+    const int qi = ys / a.n_kv, g = ys - qi * a.n_kv;
+    const int h0 = g * a.rep + sl * hp;  // the slice's first q head
     const int limit = a.cache_len + qi + 1;
     const int w0 = split * a.tw * a.tps * kTile;  // the workgroup's range [w0, w1)
     const int w1 = min(w0 + a.tw * a.tps * kTile, limit);
@@ -219,12 +227,12 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
     if (PREP) {
         const int pos = a.start_pos + qi;
         if (head && grp == 0) {
-            const int h = g * a.rep + r;
-            prep_row(qs + r * dk, a.q + (size_t)qi * a.n_heads * dk + (size_t)h * dk, dk, a.q_bias, h * dk, a.qb_len,
+            const int h = h0 + hr;
+            prep_row(qs + hr * dk, a.q + (size_t)qi * a.n_heads * dk + (size_t)h * dk, dk, a.q_bias, h * dk, a.qb_len,
                      a.q_norm, a.eps, a.freqs, a.half_dim, pos, lane);
         }
-        // the workgroup's last wave: no q head to build unless there is one group
-        // and rep fills it
+        // the workgroup's last wave; every head slice builds the row for itself,
+        // slice 0 appends it to the cache
         if (owns_new && wave == (int)(blockDim.x >> 6) - 1) {
             const size_t off = (size_t)qi * a.n_kv * dk + (size_t)g * dk;
             prep_row(nk, a.k + off, dk, a.k_bias, g * dk, a.kb_len, a.k_norm, a.eps, a.freqs, a.half_dim, pos, lane);
@@ -233,13 +241,15 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
                 float x = a.v[off + d];
                 if (a.v_bias && g * dk + d < a.vb_len) x = x + a.v_bias[g * dk + d];
                 nk[dk + d] = x;
-                a.cache_k[at + d] = nk[d];
-                a.cache_v[at + d] = x;
+                if (sl == 0) {
+                    a.cache_k[at + d] = nk[d];
+                    a.cache_v[at + d] = x;
+                }
             }
         }
     } else {
-        const float4 *qq = (const float4 *)(a.qrot + ((size_t)qi * a.n_heads + (size_t)g * a.rep) * dk);
-        for (int i = tid; i < a.rep * dk / 4; i += (int)blockDim.x) ((float4 *)qs)[i] = qq[i];
+        const float4 *qq = (const float4 *)(a.qrot + ((size_t)qi * a.n_heads + (size_t)h0) * dk);
+        for (int i = tid; i < hp * dk / 4; i += (int)blockDim.x) ((float4 *)qs)[i] = qq[i];
     }
 
     if (!FULL && one_chunk && p0 < p1) load_chunk(p0, min(kTile, p1 - p0), 0, false, true);
@@ -259,7 +269,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
             store_chunk(kreg, n, c0, newp, nk);
             __syncthreads();
             if (head && lane < n) {
-                const float *qr = qs + r * dk + c0;
+                const float *qr = qs + hr * dk + c0;
                 const float *kr = kt + lane * ks;
                 for (int d0 = 0; d0 < cw; d0 += 4 * kDotSteps) {
                     // kDotSteps 4-element steps: their LDS reads issue together,
@@ -356,7 +366,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
     // l_t * w_t, O = sum over t in order of o_t * w_t), as attn_combine_kernel does
     const int sst = dk + 2;
     if (head) {
-        float *st = mg + ((size_t)r * a.tw + grp) * sst;
+        float *st = mg + ((size_t)hr * a.tw + grp) * sst;
         if (lane == 0) {
             st[0] = m;
             st[1] = l;
@@ -369,7 +379,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
     }
     __syncthreads();
     if (!head || grp != 0) return;
-    const float *sb = mg + (size_t)r * a.tw * sst;
+    const float *sb = mg + (size_t)hr * a.tw * sst;
     float M = -INFINITY;
     for (int t = 0; t < a.tw; t++) M = fmaxf(M, sb[t * sst]);
     const bool mine = lane < a.tw;
@@ -390,7 +400,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
             O[j] = O[j] + (d < dk ? sb[t * sst + 2 + d] : 0.0f) * w;
         }
     }
-    const int h = g * a.rep + r;
+    const int h = h0 + hr;
     if (a.splits == 1) {
         const float inv = 1.0f / L;
         float *dst = a.out + ((size_t)qi * a.n_heads + h) * dk;  // mergeHeadsDataF32 layout
@@ -483,9 +493,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
 }  // namespace
 
 namespace {
-size_t attn_lds_bytes(int tw, int rep, int d_k) {
+// hp: q heads per workgroup (rep / head slices)
+size_t attn_lds_bytes(int tw, int rep, int hp, int d_k) {
     const int nh = rep > 4 ? rep : 4;
-    return ((size_t)tw * kTile * (kChunk + 4) + (size_t)(rep + 2) * d_k + (size_t)tw * rep * (d_k + 2) +
+    return ((size_t)tw * kTile * (kChunk + 4) + (size_t)(hp + 2) * d_k + (size_t)tw * hp * (d_k + 2) +
             (size_t)tw * nh * kTile) *
            sizeof(float);
 }
@@ -500,9 +511,20 @@ size_t lds_per_block() {
     }();
     return v;
 }
+// the device's CU count (read once)
+int cus_per_device() {
+    static const int v = [] {
+        int dev = 0, c = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+            return 256;
+        return c;
+    }();
+    return v;
+}
 }  // namespace
 
-void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw,
+void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw, int *hs,
                     size_t *ws_bytes) {
     const int tiles = (kv_len + kTile - 1) / kTile;
     const int pairs = seq * n_kv;
@@ -512,7 +534,7 @@ void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *sp
     int G = kMaxWaves / nh;
     G = G < T.attn_tile_groups ? G : T.attn_tile_groups;
     G = G < tiles ? G : tiles;
-    while (G > 1 && attn_lds_bytes(G, rep, d_k) > lds_per_block()) G--;
+    while (G > 1 && attn_lds_bytes(G, rep, rep, d_k) > lds_per_block()) G--;
     G = G < 1 ? 1 : G;
     int S, t;
     if (tiles <= G) {
@@ -531,9 +553,25 @@ void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *sp
         t = (tiles + S * G - 1) / (S * G);
         S = (tiles + t * G - 1) / (t * G);
     }
+    // head slices (the plan above does not depend on them, so neither do the
+    // results): while there are fewer workgroups than CUs, the q heads of a
+    // kv head are spread over up to rep / 2 workgroups (two heads or more
+    // each), every one reading the kv head's rows for its own heads; a
+    // divisor of rep. Measured (decode, 32 q / 8 kv heads, d_k 128): KV 128
+    // 10.2 -> 8.8 µs, KV 2047 15.4 -> 14.8 µs; one head per workgroup was
+    // slower (9.1 and 21.4 µs)
+    int H = T.attn_head_slices;
+    if (H <= 0) {
+        const int64_t wgs = (int64_t)pairs * S;
+        H = (int)((cus_per_device() + wgs - 1) / wgs);
+        H = H < rep / 2 ? H : rep / 2;
+    }
+    H = H < 1 ? 1 : (H > rep ? rep : H);
+    while (H > 1 && (rep % H || (int64_t)pairs * H > 65535)) H--;  // grid y: pairs x H
     *splits = S;
     *tps = t;
     *tw = G;
+    *hs = H;
     const size_t qrot = (size_t)seq * n_heads * d_k * sizeof(float);
     const size_t part = S > 1 ? (size_t)seq * n_heads * S * (d_k + 2) * sizeof(float) : 0;
     *ws_bytes = ((qrot + 255) & ~(size_t)255) + part;
@@ -557,13 +595,14 @@ void launch_split(const AttnArgs &a, dim3 grid, size_t lds, hipStream_t s) {
 }
 
 sllm_status launch_attention(const AttnArgs &a, hipStream_t s) {
-    const size_t lds = attn_lds_bytes(a.tw, a.rep, a.d_k);
+    if (a.hs < 1 || a.rep % a.hs) return set_error(SLLM_ERR_ARG, "attention: head slices must divide rep");
+    const size_t lds = attn_lds_bytes(a.tw, a.rep, a.rep / a.hs, a.d_k);
     if (a.seq == 1) {
-        launch_split<true>(a, dim3(a.splits, a.n_kv), lds, s);
+        launch_split<true>(a, dim3(a.splits, a.n_kv * a.hs), lds, s);
     } else {
         hipLaunchKernelGGL(attn_prep_kernel, dim3(a.seq, a.n_heads + a.n_kv), dim3(64), 0, s, a);
         SLLM_HIP(hipGetLastError());
-        launch_split<false>(a, dim3(a.splits, a.seq * a.n_kv), lds, s);
+        launch_split<false>(a, dim3(a.splits, a.seq * a.n_kv * a.hs), lds, s);
     }
     SLLM_HIP(hipGetLastError());
     if (a.splits > 1) {

@@ -216,9 +216,10 @@ struct AttnArgs {
     float *qrot;               // workspace: seq x n_heads x d_k
     float *part;               // workspace: seq x n_heads x splits x (d_k + 2)
     int splits, tps, tw;       // splits per (row, kv head); tile groups per split; tiles of 64 positions per group
+    int hs;                    // head slices: workgroups per (split, row, kv head), rep / hs q heads each
 };
 // Split plan and workspace bytes (qrot + partials) of an attention call.
-void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw,
+void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw, int *hs,
                     size_t *ws_bytes);
 sllm_status launch_attention(const AttnArgs &a, hipStream_t s);
 
@@ -233,6 +234,7 @@ struct Tuning {
     int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
     int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
     int attn_tile_groups = 4;      // attention: most tile groups (of max(4, rep) waves) per workgroup
+    int attn_head_slices = 0;      // attention: workgroups sharing one kv head's q heads (0: by workgroup count)
 };
 Tuning &tuning();
 

@@ -171,6 +171,27 @@ def test_tile_groups_and_splits(groups, target, cache_len):
         sq.set_param("attn_target_blocks", 512)
 
 
+@pytest.mark.parametrize("H,KV,dk,half,seq,cache_len", [
+    (8, 2, 128, 64, 1, 0), (8, 2, 128, 64, 1, 130), (8, 2, 128, 64, 1, 2047), (8, 2, 128, 64, 3, 70),
+    (32, 8, 128, 64, 1, 128), (16, 2, 64, 32, 1, 300), (6, 3, 96, 48, 1, 65), (4, 2, 64, 32, 5, 40)])
+def test_head_slices_give_the_same_bits(H, KV, dk, half, seq, cache_len):
+    # the q heads of a kv head spread over 1, 2, 4 or 8 workgroups (the
+    # planner keeps a divisor of the heads per kv head) or as many as the
+    # planner picks: every head's arithmetic is the same, so are the outputs
+    outs = []
+    try:
+        for hs in (1, 2, 4, 8, 0):
+            sq.set_param("attn_head_slices", hs)
+            rng = np.random.default_rng(H * 1000 + cache_len * 10 + seq)
+            m = Model(H, KV, dk, half, rng, base=500000.0)
+            got, _ = run_case(m, seq, cache_len, rng)
+            outs.append(got)
+    finally:
+        sq.set_param("attn_head_slices", 0)
+    for hs, o in zip((2, 4, 8, 0), outs[1:]):
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32)), hs
+
+
 def test_first_position_after_a_launch_that_leaves_nan_in_lds():
     # a tile with one row: the value loop must not multiply stale LDS rows
     # (here NaN activations a GEMV staged there) by zero weights
