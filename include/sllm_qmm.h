@@ -329,7 +329,27 @@ sllm_status sllm_debug_quantize_act(const float *x, int rows, int cols, int8_t *
 sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_rows, int x_cols,
                                   int32_t *out);
 
-/* Tuning knob for launch-shape sweeps ("gemv_grid_cap", "gemv_waves"...). */
+/*
+ * Launch-shape knobs (no counterpart in the reference: its matmuls have no
+ * launch shapes). Process-wide; set them before the calls they should
+ * affect, not while other threads are launching. Results do not depend on
+ * any of them except where noted. Unknown names or values: SLLM_ERR_ARG.
+ *   gemv_waves          4, 8, 16   most waves per GEMV workgroup (16)
+ *   gemv_wg_per_cu      1..8       GEMV workgroups per CU (1)
+ *   gemv_max_nb         1..8       most 32-element blocks per lane per unit (8)
+ *   gemv_inflight_kb    >= 64      weight bytes in flight over the device (32768)
+ *   gemv_q4k_stream     0, 1       Q4_K weights streamed from their own headers (0)
+ *   gemm_min_rows       >= 1       activation rows from which the GEMM is used (64;
+ *                                  the GEMM and GEMV sum a row's blocks in different
+ *                                  orders, so a row's last bits can change with it)
+ *   gemm_wn             0, 1, 2, 4 GEMM waves along N / 2 per workgroup (0: by tile count)
+ *   attn_target_blocks  1..65536   attention: about this many workgroups when splitting (512)
+ *   attn_tile_groups    1..4       attention: most tile groups per workgroup (4)
+ *   attn_head_slices    0..64      attention: workgroups sharing a kv head's q heads
+ *                                  (0: while the grid has fewer workgroups than CUs)
+ * The attention knobs move the summation splits of the softmax except
+ * attn_head_slices, whose results are bit-identical for any value.
+ */
 sllm_status sllm_set_param(const char *name, int value);
 
 #ifdef __cplusplus
