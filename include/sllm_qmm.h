@@ -343,6 +343,8 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)
  *   gemm_wn             0, 1, 2, 4 GEMM waves along N / 2 per workgroup (0: by tile count)
+ *   gemm_splits         0..64      GEMM K splits, added in split order (0: by tile count;
+ *                                  the split count moves the fp32 summation splits)
  *   attn_target_blocks  1..65536   attention: about this many workgroups when splitting (512)
  *   attn_tile_groups    1..4       attention: most tile groups per workgroup (4)
  *   attn_head_slices    0..64      attention: workgroups sharing a kv head's q heads

@@ -420,6 +420,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "attn_head_slices") && value >= 0 && value <= 64) t.attn_head_slices = value;
     else if (!std::strcmp(name, "gemm_wn") && (value == 0 || value == 1 || value == 2 || value == 4)) t.gemm_wn = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
+    else if (!std::strcmp(name, "gemm_splits") && value >= 0 && value <= 64) t.gemm_splits = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;

@@ -546,15 +546,19 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     GemmPlan p{};
     p.mtiles = (M + kBM - 1) / kBM;
     auto tiles = [&](int wn) { return (int64_t)p.mtiles * ((N + 32 * wn - 1) / (32 * wn)); };
-    // 8-wave workgroups once there is a tile per CU, else 4-wave ones with
-    // more K splits (measured at M = 64: Q8_0 4096x14336 50 -> 34 µs against
-    // 2-wave workgroups)
-    p.wn = tiles(4) >= cus ? 4 : 2;
+    // 8-wave workgroups (64 x 128 tiles) from 64 such tiles, else 4-wave ones;
+    // then K splits double until there are 1.5 workgroups per CU, each split
+    // keeping >= 4 stages. Measured at M = 64 / 128 (µs): Q4_1 14336x4096
+    // 44-46 -> 39-40 / 70-74 -> 62 against 4-wave tiles with 2 workgroups per
+    // CU; Q8_0 4096x14336 at M = 64 keeps 4-wave tiles (35-38; 8-wave ones
+    // 40); 2-wave workgroups were slower everywhere (Q8_0 at M = 64: 50)
+    p.wn = tiles(4) >= 64 ? 4 : 2;
     if (tuning().gemm_wn) p.wn = tuning().gemm_wn;
     p.ntiles = (N + 32 * p.wn - 1) / (32 * p.wn);
     const int nst = G / kKB;
     int S = 1;
-    while ((int64_t)p.mtiles * p.ntiles * S < 2 * cus && nst / (S * 2) >= 4) S *= 2;
+    while ((int64_t)p.mtiles * p.ntiles * S * 2 < 3 * cus && nst / (S * 2) >= 4) S *= 2;
+    if (tuning().gemm_splits) S = tuning().gemm_splits < nst ? tuning().gemm_splits : nst;
     p.splits = S;
     p.sps = (nst + S - 1) / S;
     return p;

@@ -231,6 +231,7 @@ struct Tuning {
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
     int gemm_wn = 0;           // GEMM waves along N per workgroup / 2 (1, 2, 4; 0: by tile count)
+    int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
     int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
     int attn_tile_groups = 4;      // attention: most tile groups (of max(4, rep) waves) per workgroup
