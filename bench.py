@@ -197,7 +197,7 @@ def main() -> int:
     return 0
 
 
-def time_launches(torch, stream, launch, n: int, warm: int = 8) -> float:
+def time_launches(torch, stream, launch, n: int, warm: int = 10) -> float:
     """Mean duration (us) of `launch(i)` over n back-to-back calls between two HIP
     events on the launch stream. Consecutive launches on one stream run with no
     measurable gap, so this is the kernel time rocprofv3 --kernel-trace reports
@@ -276,19 +276,19 @@ def config_table(sq, synth, torch, stream) -> dict:
     for N in (H, KV, F):
         ws = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q5_K, synth.q5k_blocks(20 + N // 1024, N, H), N, H))
         for M in (1, 64, 512):
-            table[f"C4 q5k1 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else 20)
+            table[f"C4 q5k1 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else 100)
         del ws
         ws = copies(q_from_f32("q5", 30 + N // 1024, N, H))
         for M in (1, 64, 512):
-            table[f"C4 q5 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else (20 if M == 64 else 4))
+            table[f"C4 q5 {N}x{H} M={M}"] = run(ws, M, 200 if M == 1 else 100)
         del ws
     g = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(100, F, H), F, H))
     for M in (64, 512):
-        table[f"C3 q4_1 gate {F}x{H} M={M}"] = run(g, M, 20)
+        table[f"C3 q4_1 gate {F}x{H} M={M}"] = run(g, M, 100)
     del g
     d = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q6_K, synth.q6k_blocks(102, H, F), H, F))
     for M in (64, 512):
-        table[f"C3 q8 down {H}x{F} M={M}"] = run(d, M, 20)
+        table[f"C3 q8 down {H}x{F} M={M}"] = run(d, M, 100)
     del d
     # native Q2_K / Q3_K (the reference's dense-fp32 types): GEMV over the
     # native blocks; dense_fp32_equiv_GBps counts the 4 B / weight the
