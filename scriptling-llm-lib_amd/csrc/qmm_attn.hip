@@ -2,12 +2,12 @@
 // model_f32.go:398-466) on device buffers: bias adds, per-head QK RMSNorm,
 // RoPE, the KV-cache append and the causal GQA attention with merged heads.
 //
-// attn_split_kernel: one workgroup per (split, row, kv head). A split is a
-//   range of cached positions in tiles of 64 (one per lane), shared by up to
-//   four tile groups of waves that run side by side; a group stages its
-//   tile's K and V rows in LDS once for all q heads of the kv group (GQA:
-//   the kv head is read from HBM once) and each of its waves owns one q
-//   head. The groups' softmax states are merged in LDS; with one split the
+// attn_split_kernel: one workgroup per (split, row, kv head, head slice). A
+//   split is a range of cached positions in tiles of 64 (one per lane),
+//   shared by up to three tile groups of waves that run side by side; a group
+//   stages its tile's K and V rows in LDS once for the q heads of its slice
+//   (GQA: the kv head is read from HBM once, through L2 by each slice) and
+//   each owning wave takes one q head. The groups' softmax states are merged in LDS; with one split the
 //   workgroup writes the attention output itself, otherwise the split's
 //   state goes to the workspace. Scores are the reference's sequential
 //   float32 dots. For one query row (decode) it also does the bias / norm /
