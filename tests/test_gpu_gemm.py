@@ -42,6 +42,27 @@ def test_prefill_parity(qtype, M, N, K):
     assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} M={M} {N}x{K}")
 
 
+@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1"])
+@pytest.mark.parametrize("wn,splits", [(2, 1), (2, 3), (4, 5), (4, 8), (1, 2)])
+def test_tile_width_and_split_overrides(qtype, wn, splits):
+    # any tile width and K split count gives the oracle's result within the
+    # bound (K = 1024 is 8 stages: 5 splits of 2 stages leave the last split
+    # empty, and it adds a zero tile)
+    N, K, M = 320, 1024, 130
+    raw = make_raw(qtype, N, K, seed=wn * 10 + splits)
+    x = make_x(M, K, seed=splits)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    sq.set_param("gemm_wn", wn)
+    sq.set_param("gemm_splits", splits)
+    try:
+        got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    finally:
+        sq.set_param("gemm_wn", 0)
+        sq.set_param("gemm_splits", 0)
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} wn={wn} S={splits}")
+
+
 @pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1", "q5"])
 def test_prefill_edge_activations(qtype):
     # zero rows, denormal rows and huge rows through the GEMM's quantize pre-pass
