@@ -56,6 +56,20 @@ sllm_status sllm_init(void);
 /* Message for the last failing call on this thread ("" if none). */
 const char *sllm_last_error(void);
 
+/*
+ * The per-stream device workspace (no counterpart in the reference, whose
+ * scratch comes from sync.Pools, q8q8.go:12-13): the _dev entry points keep
+ * the prefill GEMM's activation codes and split partials, the attention's
+ * q rows and split states and multi-row normed rows in a buffer owned by
+ * (device, stream), grown on demand. Growth allocates, so it cannot happen
+ * while the stream is being captured into a HIP graph (the call returns
+ * SLLM_ERR_ARG, naming the size it needed): reserve at least that many bytes
+ * with this call before capturing. A buffer that is outgrown is kept, not
+ * freed, until the process ends, so graphs captured before a growth stay
+ * valid. Growth at least doubles the buffer.
+ */
+sllm_status sllm_workspace_reserve(void *stream, size_t bytes);
+
 /* Static description: arch, plane layout version, kernel configuration. */
 const char *sllm_kernel_info(void);
 
@@ -147,7 +161,7 @@ sllm_status sllm_matmul_row_quant_into_f32(const sllm_weight *w, const float *no
  * Device-resident variant: x and dst are device pointers, work is enqueued on
  * `stream` (a hipStream_t; NULL = the default stream) and the call returns
  * without synchronising. May allocate device scratch on first use of a larger
- * shape (GEMM activation workspace).
+ * shape (the stream's workspace, see sllm_workspace_reserve).
  */
 sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x_dev, int x_rows, int x_cols,
                             float *dst_dev, void *stream);
@@ -288,6 +302,7 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
                                const float *k_dev, const float *v_dev, int seq_len, int start_pos,
                                float *out_dev, void *stream);
 
+
 /* Host-buffer form of sllm_matmul_swiglu_dev (synchronous; h only). */
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,
                                         int x_rows, int x_cols, float *h);
@@ -299,7 +314,11 @@ sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_we
  * values never winning, and 0 if logits[0] is NaN. *argmax_dev (device int)
  * receives the index; logits_dev (may be NULL) the logits. Needs
  * x_cols == Cols. Launches on the same stream are serialized; launches on
- * different streams each use their own 64-byte scratch.
+ * different streams each use their own 64-byte scratch (allocated by the
+ * first call on a stream, which therefore must not be under capture). A HIP
+ * graph captured on stream S keeps S's scratch wherever it is replayed: a
+ * replay must not overlap an argmax launch on S, nor a replay of another
+ * graph captured on S (the shared counter would misfire).
  */
 sllm_status sllm_matmul_argmax_dev(const sllm_weight *w, const float *x_dev, int x_cols, float *logits_dev,
                                    int *argmax_dev, void *stream);

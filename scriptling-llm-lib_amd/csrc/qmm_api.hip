@@ -52,12 +52,22 @@ struct Ctx {
 };
 std::vector<Ctx *> g_pool;
 
-// GEMM activation workspace per (device, stream), grown on demand.
+// Workspace per (device, stream) (GEMM activation codes and split partials,
+// attention q rows and split states, normed rows), grown on demand. A buffer
+// that is outgrown is retired, never freed while the library is loaded: a HIP
+// graph captured on the stream before the growth still holds its address and
+// may be replayed later.
 struct Ws {
     void *p = nullptr;
     size_t cap = 0;
+    std::vector<void *> retired;
 };
 std::unordered_map<uint64_t, Ws> g_ws;
+
+bool capturing(hipStream_t stream) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
 
 // Argmax scratch per (device, stream): a 64-bit key and two counters, zeroed
 // once at allocation; every argmax launch leaves them zeroed again.
@@ -70,8 +80,7 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
     std::lock_guard<std::mutex> lk(g_mu);
     void *&p = g_amax[key];
     if (!p) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        if (capturing(stream))
             return set_error(SLLM_ERR_ARG, "argmax: the first call on a stream allocates its scratch; "
                                            "make one call on the stream before capturing it");
         if (hipMalloc(&p, 64) != hipSuccess) {
@@ -86,9 +95,11 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
     return SLLM_OK;
 }
 
-// The GEMM activation workspace of `stream` on the current device, grown to at
-// least `need` bytes. Growing synchronizes the stream before freeing the old
-// buffer (work already queued on it may still read it).
+// The workspace of `stream` on the current device, grown to at least `need`
+// bytes (to at least twice its size, so retired buffers total less than the
+// live one). The old buffer is retired, not freed (work queued on the stream
+// and graphs captured on it may still use it). A stream under capture cannot
+// grow its workspace: the caller reserves it first (sllm_workspace_reserve).
 sllm_status workspace(hipStream_t stream, size_t need, void **out, size_t *cap) {
     int dev = 0;
     SLLM_HIP(hipGetDevice(&dev));
@@ -96,14 +107,16 @@ sllm_status workspace(hipStream_t stream, size_t need, void **out, size_t *cap) 
     std::lock_guard<std::mutex> lk(g_mu);
     Ws &w = g_ws[key];
     if (w.cap < need) {
-        if (w.p) {
-            SLLM_HIP(hipStreamSynchronize(stream));
-            (void)hipFree(w.p);
-            w.p = nullptr;
-            w.cap = 0;
-        }
+        if (capturing(stream))
+            return set_error(SLLM_ERR_ARG, "the stream's workspace must grow to " + std::to_string(need) +
+                                               " bytes while the stream is capturing; call "
+                                               "sllm_workspace_reserve on it before the capture");
         size_t want = need < ((size_t)4 << 20) ? ((size_t)4 << 20) : need;
-        if (hipMalloc(&w.p, want) != hipSuccess) return set_error(SLLM_ERR_OOM, "GEMM workspace allocation failed");
+        want = want < 2 * w.cap ? 2 * w.cap : want;
+        void *p = nullptr;
+        if (hipMalloc(&p, want) != hipSuccess) return set_error(SLLM_ERR_OOM, "workspace allocation failed");
+        if (w.p) w.retired.push_back(w.p);
+        w.p = p;
         w.cap = want;
     }
     *out = w.p;
@@ -369,6 +382,71 @@ bool check_shape(int rows, int cols, sllm_status *st) {
     return true;
 }
 
+// sllm_attention_dev: checks, plan, kernels; the scratch is the stream's workspace.
+sllm_status attention_impl(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q, const float *k,
+                           const float *v, int seq_len, int start_pos, float *out, hipStream_t s) {
+    if (!kv || !p || !q || !k || !v || !out) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
+    if (seq_len <= 0) return set_error(SLLM_ERR_ARG, "seq_len must be positive");
+    if (start_pos < 0) return set_error(SLLM_ERR_ARG, "start_pos must not be negative");
+    if (p->n_kv_heads != kv->n_kv || p->d_k != kv->d_k)
+        return set_error(SLLM_ERR_ARG, "n_kv_heads / d_k differ from the KV cache's");
+    if (p->n_heads <= 0 || p->n_heads % p->n_kv_heads != 0 || p->n_heads / p->n_kv_heads > 8)
+        return set_error(SLLM_ERR_SHAPE, "n_heads must be a multiple of n_kv_heads, at most 8 times it");
+    if (p->rope_half_dim < 0 || 2 * p->rope_half_dim > p->d_k)
+        return set_error(SLLM_ERR_ARG, "rope_half_dim outside 0 .. d_k / 2");
+    if (p->rope_half_dim > 0 && !p->rope_freqs) return set_error(SLLM_ERR_ARG, "null rope_freqs");
+    if (p->q_bias_len < 0 || p->k_bias_len < 0 || p->v_bias_len < 0)
+        return set_error(SLLM_ERR_ARG, "negative bias length");
+    const int cl = kv->len[(size_t)layer];
+    if ((int64_t)cl + seq_len > kv->cap) return set_error(SLLM_ERR_SHAPE, "KV cache full (max_seq rows)");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    int splits = 0, tps = 0, tw = 0, hs = 1;
+    size_t wsb = 0;
+    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &hs, &wsb);
+    void *ws = nullptr;
+    size_t cap = 0;
+    if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
+    AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.seq = seq_len;
+    a.n_heads = p->n_heads;
+    a.n_kv = kv->n_kv;
+    a.d_k = kv->d_k;
+    a.rep = p->n_heads / kv->n_kv;
+    a.q_bias = p->q_bias_len ? p->q_bias : nullptr;
+    a.k_bias = p->k_bias_len ? p->k_bias : nullptr;
+    a.v_bias = p->v_bias_len ? p->v_bias : nullptr;
+    a.qb_len = p->q_bias_len;
+    a.kb_len = p->k_bias_len;
+    a.vb_len = p->v_bias_len;
+    a.q_norm = p->q_norm_w;
+    a.k_norm = p->k_norm_w;
+    a.eps = p->norm_eps;
+    a.freqs = p->rope_freqs;
+    a.half_dim = p->rope_half_dim;
+    a.start_pos = start_pos;
+    const size_t loff = (size_t)layer * kv->n_kv * kv->cap * kv->d_k;
+    a.cache_k = kv->k + loff;
+    a.cache_v = kv->v + loff;
+    a.cap = kv->cap;
+    a.cache_len = cl;
+    a.scale = 1.0f / (float)std::sqrt((double)kv->d_k);  // fusedAttentionHeadF32, float32_ops.go:191
+    a.out = out;
+    a.qrot = (float *)ws;
+    a.part = (float *)((char *)ws + align256((size_t)seq_len * p->n_heads * kv->d_k * sizeof(float)));
+    a.splits = splits;
+    a.tps = tps;
+    a.tw = tw;
+    a.hs = hs;
+    if ((st = launch_attention(a, s)) != SLLM_OK) return st;
+    kv->len[(size_t)layer] = cl + seq_len;
+    return SLLM_OK;
+}
+
 }  // namespace
 
 sllm_status set_error(sllm_status st, const std::string &msg) {
@@ -424,6 +502,14 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;
+}
+
+sllm_status sllm_workspace_reserve(void *stream, size_t bytes) {
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    void *p = nullptr;
+    size_t cap = 0;
+    return workspace((hipStream_t)stream, bytes, &p, &cap);
 }
 
 sllm_status sllm_weight_from_quant(const char *qtype, const void *raw, size_t raw_bytes, int groups, int rows,
@@ -996,67 +1082,7 @@ sllm_status sllm_kv_cache_data(const sllm_kv_cache *kv, int layer, float **k_dev
 sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q,
                                const float *k, const float *v, int seq_len, int start_pos, float *out,
                                void *stream) {
-    if (!kv || !p || !q || !k || !v || !out) return set_error(SLLM_ERR_ARG, "null pointer");
-    if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
-    if (seq_len <= 0) return set_error(SLLM_ERR_ARG, "seq_len must be positive");
-    if (start_pos < 0) return set_error(SLLM_ERR_ARG, "start_pos must not be negative");
-    if (p->n_kv_heads != kv->n_kv || p->d_k != kv->d_k)
-        return set_error(SLLM_ERR_ARG, "n_kv_heads / d_k differ from the KV cache's");
-    if (p->n_heads <= 0 || p->n_heads % p->n_kv_heads != 0 || p->n_heads / p->n_kv_heads > 8)
-        return set_error(SLLM_ERR_SHAPE, "n_heads must be a multiple of n_kv_heads, at most 8 times it");
-    if (p->rope_half_dim < 0 || 2 * p->rope_half_dim > p->d_k)
-        return set_error(SLLM_ERR_ARG, "rope_half_dim outside 0 .. d_k / 2");
-    if (p->rope_half_dim > 0 && !p->rope_freqs) return set_error(SLLM_ERR_ARG, "null rope_freqs");
-    if (p->q_bias_len < 0 || p->k_bias_len < 0 || p->v_bias_len < 0)
-        return set_error(SLLM_ERR_ARG, "negative bias length");
-    const int cl = kv->len[(size_t)layer];
-    if ((int64_t)cl + seq_len > kv->cap) return set_error(SLLM_ERR_SHAPE, "KV cache full (max_seq rows)");
-    sllm_status st = ensure_init();
-    if (st != SLLM_OK) return st;
-    hipStream_t s = (hipStream_t)stream;
-    int splits = 0, tps = 0, tw = 0, hs = 1;
-    size_t wsb = 0;
-    attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &hs, &wsb);
-    void *ws = nullptr;
-    size_t cap = 0;
-    if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
-    AttnArgs a{};
-    a.q = q;
-    a.k = k;
-    a.v = v;
-    a.seq = seq_len;
-    a.n_heads = p->n_heads;
-    a.n_kv = kv->n_kv;
-    a.d_k = kv->d_k;
-    a.rep = p->n_heads / kv->n_kv;
-    a.q_bias = p->q_bias_len ? p->q_bias : nullptr;
-    a.k_bias = p->k_bias_len ? p->k_bias : nullptr;
-    a.v_bias = p->v_bias_len ? p->v_bias : nullptr;
-    a.qb_len = p->q_bias_len;
-    a.kb_len = p->k_bias_len;
-    a.vb_len = p->v_bias_len;
-    a.q_norm = p->q_norm_w;
-    a.k_norm = p->k_norm_w;
-    a.eps = p->norm_eps;
-    a.freqs = p->rope_freqs;
-    a.half_dim = p->rope_half_dim;
-    a.start_pos = start_pos;
-    const size_t loff = (size_t)layer * kv->n_kv * kv->cap * kv->d_k;
-    a.cache_k = kv->k + loff;
-    a.cache_v = kv->v + loff;
-    a.cap = kv->cap;
-    a.cache_len = cl;
-    a.scale = 1.0f / (float)std::sqrt((double)kv->d_k);  // fusedAttentionHeadF32, float32_ops.go:191
-    a.out = out;
-    a.qrot = (float *)ws;
-    a.part = (float *)((char *)ws + align256((size_t)seq_len * p->n_heads * kv->d_k * sizeof(float)));
-    a.splits = splits;
-    a.tps = tps;
-    a.tw = tw;
-    a.hs = hs;
-    if ((st = launch_attention(a, s)) != SLLM_OK) return st;
-    kv->len[(size_t)layer] = cl + seq_len;
-    return SLLM_OK;
+    return attention_impl(kv, layer, p, q, k, v, seq_len, start_pos, out, (hipStream_t)stream);
 }
 
 }  // extern "C"

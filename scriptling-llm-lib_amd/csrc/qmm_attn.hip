@@ -173,7 +173,7 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
     float *ew = mg + (size_t)hp * a.tw * (dk + 2) + (size_t)wave * kTile;  // this wave's tile weights
     const int split = blockIdx.x;
     const int ys = blockIdx.y / a.hs, sl = blockIdx.y - ys * a.hs;  // (row, kv head), head slice
-    const int qi = ys / a.n_kv, g = ys - qi * a.n_kv;
+    const int qi = a.row0 + ys / a.n_kv, g = ys - (ys / a.n_kv) * a.n_kv;
     const int h0 = g * a.rep + sl * hp;  // the slice's first q head
     const int limit = a.cache_len + qi + 1;
     const int w0 = split * a.tw * a.tps * kTile;  // the workgroup's range [w0, w1)
@@ -598,13 +598,25 @@ sllm_status launch_attention(const AttnArgs &a, hipStream_t s) {
     if (a.hs < 1 || a.rep % a.hs) return set_error(SLLM_ERR_ARG, "attention: head slices must divide rep");
     const size_t lds = attn_lds_bytes(a.tw, a.rep, a.rep / a.hs, a.d_k);
     if (a.seq == 1) {
-        launch_split<true>(a, dim3(a.splits, a.n_kv * a.hs), lds, s);
+        AttnArgs b = a;
+        b.row0 = 0;
+        launch_split<true>(b, dim3(a.splits, a.n_kv * a.hs), lds, s);
+        SLLM_HIP(hipGetLastError());
     } else {
         hipLaunchKernelGGL(attn_prep_kernel, dim3(a.seq, a.n_heads + a.n_kv), dim3(64), 0, s, a);
         SLLM_HIP(hipGetLastError());
-        launch_split<false>(a, dim3(a.splits, a.seq * a.n_kv * a.hs), lds, s);
+        // grid y is (row, kv head, head slice), at most 65535: long prefills
+        // run in chunks of rows (every row's k / v is already in the cache)
+        const int per = 65535 / (a.n_kv * a.hs);
+        if (per < 1) return set_error(SLLM_ERR_SHAPE, "attention: n_kv_heads x head slices exceeds the grid");
+        for (int r0 = 0; r0 < a.seq; r0 += per) {
+            AttnArgs b = a;
+            b.row0 = r0;
+            const int rows = a.seq - r0 < per ? a.seq - r0 : per;
+            launch_split<false>(b, dim3(a.splits, rows * a.n_kv * a.hs), lds, s);
+            SLLM_HIP(hipGetLastError());
+        }
     }
-    SLLM_HIP(hipGetLastError());
     if (a.splits > 1) {
         hipLaunchKernelGGL(attn_combine_kernel, dim3((a.seq * a.n_heads + 3) / 4), dim3(256), 0, s, a);
         SLLM_HIP(hipGetLastError());

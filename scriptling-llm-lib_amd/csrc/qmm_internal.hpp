@@ -217,6 +217,7 @@ struct AttnArgs {
     float *part;               // workspace: seq x n_heads x splits x (d_k + 2)
     int splits, tps, tw;       // splits per (row, kv head); tile groups per split; tiles of 64 positions per group
     int hs;                    // head slices: workgroups per (split, row, kv head), rep / hs q heads each
+    int row0;                  // first query row of a split-kernel launch (long prefills run in row chunks)
 };
 // Split plan and workspace bytes (qrot + partials) of an attention call.
 void attention_plan(int seq, int n_heads, int n_kv, int d_k, int kv_len, int *splits, int *tps, int *tw, int *hs,

@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
     L.sllm_kv_cache_set_length.argtypes = [P, i32]
     L.sllm_kv_cache_data.argtypes = [P, i32, C.POINTER(P), C.POINTER(P)]
     L.sllm_attention_dev.argtypes = [P, i32, C.POINTER(AttnParams), P, P, P, i32, i32, P, P]
+    L.sllm_workspace_reserve.argtypes = [P, sz]
     for name in exported_names():  # raises AttributeError if a declared symbol is missing
         f = getattr(L, name)
         if name in ("sllm_last_error", "sllm_kernel_info"):
@@ -401,6 +402,11 @@ def attention_dev(kv: KVCache, layer: int, params: AttnParams, q_ptr: int, k_ptr
     _check(lib().sllm_attention_dev(kv.handle, layer, C.byref(params), C.c_void_p(q_ptr), C.c_void_p(k_ptr),
                                     C.c_void_p(v_ptr), seq_len, start_pos, C.c_void_p(out_ptr),
                                     C.c_void_p(stream)))
+
+
+def workspace_reserve(stream: int, nbytes: int) -> None:
+    """Grow the stream's device workspace to at least nbytes now (before a graph capture)."""
+    _check(lib().sllm_workspace_reserve(C.c_void_p(stream), int(nbytes)))
 
 
 def argmax_f32_dev(v_ptr: int, n: int, stream: int = 0) -> int:

@@ -284,3 +284,12 @@ def test_matmul_add_is_matmul_then_one_add(qtype, M):
     torch.cuda.synchronize()
     want = base + plain.cpu().numpy()  # one float32 add per element
     assert np.array_equal(dst.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.slow
+def test_prefill_rows_beyond_the_grid_limit():
+    # seq_len x n_kv_heads above 65535 (the split kernel's grid y): the rows
+    # run in chunks, each against the whole cache the prep kernel filled
+    rng = np.random.default_rng(5)
+    m = Model(64, 64, 8, 4, rng)
+    run_case(m, 1030, 0, rng, layer=0, n_layers=2)
