@@ -302,6 +302,24 @@ sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_par
                                const float *k_dev, const float *v_dev, int seq_len, int start_pos,
                                float *out_dev, void *stream);
 
+/*
+ * No counterpart in the reference. For callers that cannot allocate device
+ * memory: code under HIP graph capture (without a warm-up call on the
+ * stream), serving loops and harnesses that forbid hipMalloc. The same
+ * attention as sllm_attention_dev (same kernels, bit-identical outputs), but
+ * its scratch - the rotated q rows and the split states - lives in a static
+ * 8 MiB device array per GPU, held until the process ends, so the call
+ * allocates nothing and never touches the stream's workspace. Calls that
+ * need more scratch than that (about seq_len x n_heads x (d_k x 4 bytes) for
+ * the q rows, plus the split states of long caches; a decode step of a
+ * 64-head model at 8K positions needs about 2 MiB) return SLLM_ERR_SHAPE.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (different streams, or graph replays running concurrently) race and
+ * give wrong results; serialize them.
+ */
+sllm_status sllm_attention_noalloc_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p,
+                                       const float *q_dev, const float *k_dev, const float *v_dev, int seq_len,
+                                       int start_pos, float *out_dev, void *stream);
 
 /* Host-buffer form of sllm_matmul_swiglu_dev (synchronous; h only). */
 sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_weight *w_up, const float *x,

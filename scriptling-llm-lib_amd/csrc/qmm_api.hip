@@ -124,6 +124,39 @@ sllm_status workspace(hipStream_t stream, size_t need, void **out, size_t *cap) 
     return SLLM_OK;
 }
 
+// The scratch of sllm_attention_noalloc_dev: the attention's rotated q rows
+// and split states, which sllm_attention_dev keeps in the stream's
+// workspace, in a static device array so that the call allocates nothing.
+// Every GPU holds its own copy until the process ends. In host code
+// `scratch` only names the array (its host shadow): its device address on
+// each GPU comes from hipGetSymbolAddress, looked up once per device with
+// that device current, and kept in g_scratch. Nothing in it needs to start at
+// zero: every call writes the q rows and split states it reads.
+constexpr size_t kStaticScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+std::unordered_map<int, void *> g_scratch;  // device -> address of its scratch
+
+// The current device's scratch address; g_mu held.
+sllm_status static_scratch_locked(int dev, void **out) {
+    auto it = g_scratch.find(dev);
+    if (it == g_scratch.end()) {
+        void *p = nullptr;
+        hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return set_error(SLLM_ERR_DEVICE, "hipGetSymbolAddress(scratch) returned no address");
+        it = g_scratch.emplace(dev, p).first;
+    }
+    *out = it->second;
+    return SLLM_OK;
+}
+
+sllm_status static_scratch(void **out) {
+    int dev = 0;
+    SLLM_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_mu);
+    return static_scratch_locked(dev, out);
+}
+
 sllm_status ensure_init() {
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_init_done) {
@@ -151,6 +184,14 @@ sllm_status ensure_init() {
         g_init_status = SLLM_ERR_DEVICE;
         g_init_msg = std::string("device is ") + prop.gcnArchName + ", this build targets gfx950 only";
         return set_error(g_init_status, g_init_msg);
+    }
+    // the static scratch of the current device (other devices: at their first call)
+    void *scr = nullptr;
+    sllm_status st = static_scratch_locked(dev, &scr);
+    if (st != SLLM_OK) {
+        g_init_status = st;
+        g_init_msg = g_err;
+        return st;
     }
     g_init_status = SLLM_OK;
     return SLLM_OK;
@@ -382,9 +423,11 @@ bool check_shape(int rows, int cols, sllm_status *st) {
     return true;
 }
 
-// sllm_attention_dev: checks, plan, kernels; the scratch is the stream's workspace.
+// sllm_attention_dev and, noalloc, sllm_attention_noalloc_dev: the same
+// checks, plan and kernels; the scratch is the stream's workspace or the
+// device's static array.
 sllm_status attention_impl(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q, const float *k,
-                           const float *v, int seq_len, int start_pos, float *out, hipStream_t s) {
+                           const float *v, int seq_len, int start_pos, float *out, hipStream_t s, bool noalloc) {
     if (!kv || !p || !q || !k || !v || !out) return set_error(SLLM_ERR_ARG, "null pointer");
     if (layer < 0 || layer >= kv->n_layers) return set_error(SLLM_ERR_ARG, "layer out of range");
     if (seq_len <= 0) return set_error(SLLM_ERR_ARG, "seq_len must be positive");
@@ -407,7 +450,16 @@ sllm_status attention_impl(sllm_kv_cache *kv, int layer, const sllm_attn_params 
     attention_plan(seq_len, p->n_heads, kv->n_kv, kv->d_k, cl + seq_len, &splits, &tps, &tw, &hs, &wsb);
     void *ws = nullptr;
     size_t cap = 0;
-    if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) return st;
+    if (noalloc) {
+        if (wsb > kStaticScratchBytes)
+            return set_error(SLLM_ERR_SHAPE, "attention needs " + std::to_string(wsb) +
+                                                 " bytes of scratch, more than the static scratch's " +
+                                                 std::to_string(kStaticScratchBytes) +
+                                                 " (fewer rows per call, or sllm_attention_dev)");
+        if ((st = static_scratch(&ws)) != SLLM_OK) return st;
+    } else if ((st = workspace(s, wsb, &ws, &cap)) != SLLM_OK) {
+        return st;
+    }
     AttnArgs a{};
     a.q = q;
     a.k = k;
@@ -1082,7 +1134,13 @@ sllm_status sllm_kv_cache_data(const sllm_kv_cache *kv, int layer, float **k_dev
 sllm_status sllm_attention_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q,
                                const float *k, const float *v, int seq_len, int start_pos, float *out,
                                void *stream) {
-    return attention_impl(kv, layer, p, q, k, v, seq_len, start_pos, out, (hipStream_t)stream);
+    return attention_impl(kv, layer, p, q, k, v, seq_len, start_pos, out, (hipStream_t)stream, false);
+}
+
+sllm_status sllm_attention_noalloc_dev(sllm_kv_cache *kv, int layer, const sllm_attn_params *p, const float *q,
+                                       const float *k, const float *v, int seq_len, int start_pos, float *out,
+                                       void *stream) {
+    return attention_impl(kv, layer, p, q, k, v, seq_len, start_pos, out, (hipStream_t)stream, true);
 }
 
 }  // extern "C"

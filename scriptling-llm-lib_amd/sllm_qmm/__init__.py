@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
     L.sllm_kv_cache_set_length.argtypes = [P, i32]
     L.sllm_kv_cache_data.argtypes = [P, i32, C.POINTER(P), C.POINTER(P)]
     L.sllm_attention_dev.argtypes = [P, i32, C.POINTER(AttnParams), P, P, P, i32, i32, P, P]
+    L.sllm_attention_noalloc_dev.argtypes = [P, i32, C.POINTER(AttnParams), P, P, P, i32, i32, P, P]
     L.sllm_workspace_reserve.argtypes = [P, sz]
     for name in exported_names():  # raises AttributeError if a declared symbol is missing
         f = getattr(L, name)
@@ -402,6 +403,16 @@ def attention_dev(kv: KVCache, layer: int, params: AttnParams, q_ptr: int, k_ptr
     _check(lib().sllm_attention_dev(kv.handle, layer, C.byref(params), C.c_void_p(q_ptr), C.c_void_p(k_ptr),
                                     C.c_void_p(v_ptr), seq_len, start_pos, C.c_void_p(out_ptr),
                                     C.c_void_p(stream)))
+
+
+def attention_noalloc_dev(kv: KVCache, layer: int, params: AttnParams, q_ptr: int, k_ptr: int, v_ptr: int,
+                          seq_len: int, start_pos: int, out_ptr: int, stream: int = 0) -> None:
+    """attention_dev with its scratch in the library's static device array:
+    allocates nothing (usable under graph capture without a warm-up call);
+    calls that overlap on one GPU race."""
+    _check(lib().sllm_attention_noalloc_dev(kv.handle, layer, C.byref(params), C.c_void_p(q_ptr),
+                                            C.c_void_p(k_ptr), C.c_void_p(v_ptr), seq_len, start_pos,
+                                            C.c_void_p(out_ptr), C.c_void_p(stream)))
 
 
 def workspace_reserve(stream: int, nbytes: int) -> None:
