@@ -9,6 +9,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsllm_qmm.so")
+# Measurement-only probe (peak int8 MFMA rate), loaded by bench.py, never by the library.
+PROBE_LIB = os.path.join(HERE, "libsllm_probe.so")
+PROBE_SOURCE = "probe_mfma.hip"
 
 SOURCES = ["qmm_api.hip", "qmm_gemv.hip", "qmm_gemv_q8.hip", "qmm_gemv_q4.hip", "qmm_gemv_q4_1.hip",
            "qmm_gemv_q5.hip", "qmm_gemv_q5k1.hip", "qmm_gemv_q4k.hip", "qmm_gemv_q2k.hip", "qmm_gemv_q3k.hip", "qmm_gemm.hip", "qmm_pack.hip", "qmm_attn.hip"]
@@ -57,6 +60,11 @@ def build(verbose: bool = False) -> str:
         list(ex.map(_run, cmds))
     _run([hipcc, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", LIB + ".tmp"])
     os.replace(LIB + ".tmp", LIB)
+    probe = [hipcc, *HIPCC_FLAGS, "-shared", os.path.join(CSRC, PROBE_SOURCE), "-o", PROBE_LIB + ".tmp"]
+    if verbose:
+        print(" ".join(probe), flush=True)
+    _run(probe)
+    os.replace(PROBE_LIB + ".tmp", PROBE_LIB)
     return LIB
 
 

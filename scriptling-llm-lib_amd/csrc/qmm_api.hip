@@ -42,15 +42,24 @@ bool g_init_done = false;
 sllm_status g_init_status = SLLM_ERR_DEVICE;
 std::string g_init_msg;
 
-// Per-call resources for the host-pointer entry points: a stream and device
-// staging buffers, pooled so concurrent callers never share one.
+// Per-call resources for the host-pointer entry points: a stream, device
+// staging buffers and pinned host bounce buffers, pooled so concurrent
+// callers never share one.
 struct Ctx {
     int device = 0;
     hipStream_t stream = nullptr;
     void *buf = nullptr;
     size_t cap = 0;
+    void *hbuf = nullptr;  // pinned host memory (hipHostMalloc)
+    size_t hcap = 0;
 };
 std::vector<Ctx *> g_pool;
+
+// Host transfers of a call at most this large go through the context's
+// pinned bounce buffer (a host memcpy plus a DMA from / to pinned memory,
+// instead of the runtime staging pageable memory itself); larger ones are
+// copied from / to the caller's pageable memory directly.
+constexpr size_t kMaxPinnedBytes = (size_t)64 << 20;
 
 // Workspace per (device, stream) (GEMM activation codes and split partials,
 // attention q rows and split states, normed rows), grown on demand. A buffer
@@ -72,6 +81,7 @@ bool capturing(hipStream_t stream) {
 // Argmax scratch per (device, stream): a 64-bit key and two counters, zeroed
 // once at allocation; every argmax launch leaves them zeroed again.
 std::unordered_map<uint64_t, void *> g_amax;
+constexpr size_t kLaunchScratchBytes = 64;
 
 sllm_status amax_scratch(hipStream_t stream, void **out) {
     int dev = 0;
@@ -83,13 +93,13 @@ sllm_status amax_scratch(hipStream_t stream, void **out) {
         if (capturing(stream))
             return set_error(SLLM_ERR_ARG, "argmax: the first call on a stream allocates its scratch; "
                                            "make one call on the stream before capturing it");
-        if (hipMalloc(&p, 64) != hipSuccess) {
+        if (hipMalloc(&p, kLaunchScratchBytes) != hipSuccess) {
             p = nullptr;
             return set_error(SLLM_ERR_OOM, "argmax scratch allocation failed");
         }
         // cleared on the stream that uses it: a non-blocking stream is not
         // ordered after the null stream, where hipMemset would run
-        SLLM_HIP(hipMemsetAsync(p, 0, 64, stream));
+        SLLM_HIP(hipMemsetAsync(p, 0, kLaunchScratchBytes, stream));
     }
     *out = p;
     return SLLM_OK;
@@ -272,6 +282,82 @@ sllm_status alloc_weight(int fmt, int rows, int cols, sllm_weight **out, int lay
     }
     carve_planes(w->layout, nb, w->base, &w->planes);
     *out = w;
+    return SLLM_OK;
+}
+
+// The context's pinned buffer, grown to at least `bytes` (false: larger than
+// kMaxPinnedBytes, or pinned memory is not available).
+bool pinned(Ctx *c, size_t bytes) {
+    if (bytes > kMaxPinnedBytes) return false;
+    if (c->hcap >= bytes) return true;
+    if (c->hbuf) (void)hipHostFree(c->hbuf);
+    c->hbuf = nullptr;
+    c->hcap = 0;
+    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    if (hipHostMalloc(&c->hbuf, want, hipHostMallocDefault) != hipSuccess) {
+        c->hbuf = nullptr;
+        return false;
+    }
+    c->hcap = want;
+    return true;
+}
+
+// One host-buffer call: copy the inputs (host -> device staging), run
+// `launch` on the context's stream, copy the outputs back (device -> host)
+// and wait for the stream. Small transfers bounce through pinned memory.
+struct HostIn {
+    const void *src;
+    void *dev;
+    size_t bytes;
+};
+struct HostOut {
+    void *dst;
+    const void *dev;
+    size_t bytes;
+};
+template <class F>
+sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int nout, F launch) {
+    size_t tin = 0, tout = 0;
+    for (int i = 0; i < nin; i++) tin += (in[i].bytes + 255) & ~(size_t)255;
+    for (int i = 0; i < nout; i++) tout += (out[i].bytes + 255) & ~(size_t)255;
+    const bool pin = pinned(c, tin + tout);
+    char *hb = (char *)c->hbuf;
+    hipError_t e = hipSuccess;
+    size_t off = 0;
+    for (int i = 0; i < nin && e == hipSuccess; i++) {
+        if (pin) {
+            std::memcpy(hb + off, in[i].src, in[i].bytes);
+            e = hipMemcpyAsync(in[i].dev, hb + off, in[i].bytes, hipMemcpyHostToDevice, c->stream);
+            off += (in[i].bytes + 255) & ~(size_t)255;
+        } else {
+            e = hipMemcpyAsync(in[i].dev, in[i].src, in[i].bytes, hipMemcpyHostToDevice, c->stream);
+        }
+    }
+    if (e != hipSuccess) return hip_error(e, "host-to-device copy");
+    sllm_status st = launch();
+    if (st != SLLM_OK) {
+        (void)hipStreamSynchronize(c->stream);  // the inputs' copies still read the bounce buffer
+        return st;
+    }
+    const size_t obase = off;
+    for (int i = 0; i < nout && e == hipSuccess; i++) {
+        if (pin) {
+            e = hipMemcpyAsync(hb + off, out[i].dev, out[i].bytes, hipMemcpyDeviceToHost, c->stream);
+            off += (out[i].bytes + 255) & ~(size_t)255;
+        } else {
+            e = hipMemcpyAsync(out[i].dst, out[i].dev, out[i].bytes, hipMemcpyDeviceToHost, c->stream);
+        }
+    }
+    const hipError_t es = hipStreamSynchronize(c->stream);
+    if (e == hipSuccess) e = es;
+    if (e != hipSuccess) return hip_error(e, "device-to-host copy");
+    if (pin) {
+        off = obase;
+        for (int i = 0; i < nout; i++) {
+            std::memcpy(out[i].dst, hb + off, out[i].bytes);
+            off += (out[i].bytes + 255) & ~(size_t)255;
+        }
+    }
     return SLLM_OK;
 }
 
@@ -774,16 +860,10 @@ sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *t
     if ((st = acquire(&c, ooff + 256)) != SLLM_OK) return st;
     float *dx = (float *)c->buf;
     int *dout = (int *)((char *)c->buf + ooff);
-    hipError_t e = hipMemcpyAsync(dx, normed, xb, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) {
-        st = sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, dout, c->stream);
-        if (st == SLLM_OK) {
-            e = hipMemcpyAsync(token, dout, sizeof(int), hipMemcpyDeviceToHost, c->stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-        }
-    }
+    const HostIn in{normed, dx, xb};
+    const HostOut out{token, dout, sizeof(int)};
+    st = host_call(c, &in, 1, &out, 1, [&] { return sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, dout, c->stream); });
     release(c);
-    if (e != hipSuccess) return hip_error(e, "argmax transfer");
     return st;
 }
 
@@ -839,16 +919,12 @@ sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *wg, const sllm_weight
     if ((st = acquire(&c, hoff + hb)) != SLLM_OK) return st;
     float *dx = (float *)c->buf;
     float *dh = (float *)((char *)c->buf + hoff);
-    hipError_t e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) {
-        st = sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, dh, nullptr, nullptr, c->stream);
-        if (st == SLLM_OK) {
-            e = hipMemcpyAsync(h, dh, hb, hipMemcpyDeviceToHost, c->stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-        }
-    }
+    const HostIn in{x, dx, xb};
+    const HostOut out{h, dh, hb};
+    st = host_call(c, &in, 1, &out, 1, [&] {
+        return sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, dh, nullptr, nullptr, c->stream);
+    });
     release(c);
-    if (e != hipSuccess) return hip_error(e, "swiglu transfer");
     return st;
 }
 
@@ -865,16 +941,10 @@ sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int
     if ((st = acquire(&c, yoff + yb)) != SLLM_OK) return st;
     float *dx = (float *)c->buf;
     float *dy = (float *)((char *)c->buf + yoff);
-    hipError_t e = hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) {
-        st = sllm_matmul_dev(w, dx, x_rows, x_cols, dy, c->stream);
-        if (st == SLLM_OK) {
-            e = hipMemcpyAsync(dst, dy, yb, hipMemcpyDeviceToHost, c->stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
-        }
-    }
+    const HostIn in{x, dx, xb};
+    const HostOut out{dst, dy, yb};
+    st = host_call(c, &in, 1, &out, 1, [&] { return sllm_matmul_dev(w, dx, x_rows, x_cols, dy, c->stream); });
     release(c);
-    if (e != hipSuccess) return hip_error(e, "matmul transfer");
     return st;
 }
 
@@ -953,17 +1023,16 @@ sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int c
     Ctx *c = nullptr;
     if ((st = acquire(&c, total)) != SLLM_OK) return st;
     std::vector<float *> dd((size_t)count);
-    for (int i = 0; i < count; i++) dd[(size_t)i] = (float *)((char *)c->buf + off[(size_t)i]);
-    hipError_t e = hipMemcpyAsync(c->buf, x, xb, hipMemcpyHostToDevice, c->stream);
-    if (e == hipSuccess) {
-        st = sllm_matmul_multi_dev(ws, count, (const float *)c->buf, x_rows, x_cols, dd.data(), c->stream);
-        for (int i = 0; st == SLLM_OK && e == hipSuccess && i < count; i++)
-            e = hipMemcpyAsync(dst[i], dd[(size_t)i], (size_t)x_rows * ws[i]->rows * sizeof(float),
-                               hipMemcpyDeviceToHost, c->stream);
-        if (st == SLLM_OK && e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    std::vector<HostOut> outs((size_t)count);
+    for (int i = 0; i < count; i++) {
+        dd[(size_t)i] = (float *)((char *)c->buf + off[(size_t)i]);
+        outs[(size_t)i] = HostOut{dst[i], dd[(size_t)i], (size_t)x_rows * ws[i]->rows * sizeof(float)};
     }
+    const HostIn in{x, c->buf, xb};
+    st = host_call(c, &in, 1, outs.data(), count, [&] {
+        return sllm_matmul_multi_dev(ws, count, (const float *)c->buf, x_rows, x_cols, dd.data(), c->stream);
+    });
     release(c);
-    if (e != hipSuccess) return hip_error(e, "matmul transfer");
     return st;
 }
 

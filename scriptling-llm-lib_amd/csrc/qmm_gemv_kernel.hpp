@@ -457,36 +457,49 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int row) {
 // max per workgroup; the last workgroup to finish writes the index and
 // clears the scratch for the next launch. If row 0 is NaN the answer is 0
 // (no value compares greater than the reference's starting NaN).
+//
+// Ordering without fences: device-scope read-modify-write atomics are
+// performed at the device's coherence point (every XCD's workgroups count on
+// the one counter), and one that has returned its old value has been
+// performed. Thread 0 issues the count only once its max (and NaN flag) have
+// returned - the count's operand is passed through an empty asm that takes
+// their results as inputs, so the wave waits for them first - and the last
+// workgroup reads and clears the scratch with atomic exchanges, which see
+// every max that was performed before the counts it observed. A fence here
+// would write back and invalidate the XCD's L2 (buffer_wbl2 / buffer_inv):
+// measured, several microseconds over a launch's workgroups.
 __device__ __forceinline__ void argmax_tail(const SegTable &S, float v, bool mine, int row) {
     __shared__ unsigned long long slot[16];
+    __shared__ int nan_row0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+    if (threadIdx.x == 0) nan_row0 = 0;
     unsigned long long k = (mine && !__builtin_isnan(v)) ? argmax_key(v, row) : 0ull;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const unsigned long long o = __shfl_xor(k, off, 64);
         k = o > k ? o : k;
     }
-    if (mine && row == 0 && __builtin_isnan(v)) atomicOr(&S.amax_cnt[1], 1u);
+    __syncthreads();  // nan_row0 cleared before any wave sets it
+    if (mine && row == 0 && __builtin_isnan(v)) nan_row0 = 1;
     if (lane == 0) slot[wave] = k;
     __syncthreads();
     if (threadIdx.x == 0) {
         unsigned long long best = 0;
         for (int w = 0; w < W; w++) best = slot[w] > best ? slot[w] : best;
-        if (best) atomicMax(S.amax_key, best);
-        __threadfence();
-        if (atomicAdd(&S.amax_cnt[0], 1u) == gridDim.x - 1) {
-            // every other workgroup's max landed before its count (fence, then
-            // count). Key and flag are read with device-scope atomic loads
-            // issued together, and cleared with device-scope atomic stores
-            // (the next launch on this stream starts after this one completes)
-            __threadfence();
+        unsigned long long r1 = 0;
+        unsigned int r2 = 0;
+        if (best) r1 = __hip_atomic_fetch_max(S.amax_key, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (nan_row0) r2 = __hip_atomic_fetch_or(&S.amax_cnt[1], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned int one = 1u;
+        asm volatile("" : "+v"(one) : "v"(r1), "v"(r2));  // waits for both to return
+        if (__hip_atomic_fetch_add(&S.amax_cnt[0], one, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+            gridDim.x - 1) {
             const unsigned long long fin =
-                __hip_atomic_load(S.amax_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const unsigned int nan0 = __hip_atomic_load(&S.amax_cnt[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_exchange(S.amax_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const unsigned int nan0 =
+                __hip_atomic_exchange(&S.amax_cnt[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             *S.amax_out = (nan0 || fin == 0) ? 0 : (int)~(uint32_t)fin;
-            __hip_atomic_store(S.amax_key, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&S.amax_cnt[1], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&S.amax_cnt[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            (void)__hip_atomic_exchange(&S.amax_cnt[0], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
