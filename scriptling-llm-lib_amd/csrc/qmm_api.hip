@@ -2,6 +2,7 @@
 // stand in for the reference's Go matmul functions, and verification hooks.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -52,6 +53,8 @@ struct Ctx {
     size_t cap = 0;
     void *hbuf = nullptr;  // pinned host memory (hipHostMalloc)
     size_t hcap = 0;
+    unsigned *flag = nullptr;  // coherent pinned word: the stream writes seq there when a call's work is done
+    unsigned seq = 0;
 };
 std::vector<Ctx *> g_pool;
 
@@ -60,6 +63,13 @@ std::vector<Ctx *> g_pool;
 // instead of the runtime staging pageable memory itself); larger ones are
 // copied from / to the caller's pageable memory directly.
 constexpr size_t kMaxPinnedBytes = (size_t)64 << 20;
+// Outputs of a call at most this large (together) are written by the kernels
+// straight into the pinned buffer (device-visible host memory), without a
+// device-to-host copy.
+constexpr size_t kDirectOutBytes = (size_t)1 << 20;
+// How long a call spins on its completion word before it blocks in
+// hipStreamSynchronize instead (long calls, or a stream in error).
+constexpr double kSpinSeconds = 2e-3;
 
 // Workspace per (device, stream) (GEMM activation codes and split partials,
 // attention q rows and split states, normed rows), grown on demand. A buffer
@@ -302,9 +312,34 @@ bool pinned(Ctx *c, size_t bytes) {
     return true;
 }
 
+// Wait for everything enqueued on the context's stream. The stream writes
+// the next sequence number into the context's coherent pinned word once all
+// earlier work on it has completed (hipStreamWriteValue32) and the caller
+// spins on that word: about 4 µs less per call than hipStreamSynchronize.
+// Past kSpinSeconds, or when the word cannot be used, the call blocks in
+// hipStreamSynchronize, which also reports a failed stream.
+hipError_t wait_stream(Ctx *c) {
+    if (!c->flag && hipHostMalloc((void **)&c->flag, 64, hipHostMallocCoherent) != hipSuccess) c->flag = nullptr;
+    if (c->flag) {
+        const unsigned want = ++c->seq;
+        if (hipStreamWriteValue32(c->stream, c->flag, want, 0) == hipSuccess) {
+            const auto t0 = std::chrono::steady_clock::now();
+            for (unsigned it = 1;; it++) {
+                if (__atomic_load_n(c->flag, __ATOMIC_ACQUIRE) == want) return hipSuccess;
+                if ((it & 1023) == 0 &&
+                    std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count() > kSpinSeconds)
+                    break;
+            }
+        }
+    }
+    return hipStreamSynchronize(c->stream);
+}
+
 // One host-buffer call: copy the inputs (host -> device staging), run
-// `launch` on the context's stream, copy the outputs back (device -> host)
-// and wait for the stream. Small transfers bounce through pinned memory.
+// `launch` on the context's stream, bring the outputs back and wait for the
+// stream. Small transfers bounce through pinned memory; small outputs are
+// written by the kernels into the pinned buffer itself. launch(oaddr) gets
+// the device-visible address each output is to be written to.
 struct HostIn {
     const void *src;
     void *dev;
@@ -312,7 +347,7 @@ struct HostIn {
 };
 struct HostOut {
     void *dst;
-    const void *dev;
+    void *dev;  // device staging for the output (used unless it is written to pinned memory)
     size_t bytes;
 };
 template <class F>
@@ -321,6 +356,7 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
     for (int i = 0; i < nin; i++) tin += (in[i].bytes + 255) & ~(size_t)255;
     for (int i = 0; i < nout; i++) tout += (out[i].bytes + 255) & ~(size_t)255;
     const bool pin = pinned(c, tin + tout);
+    const bool direct = pin && tout <= kDirectOutBytes;
     char *hb = (char *)c->hbuf;
     hipError_t e = hipSuccess;
     size_t off = 0;
@@ -334,13 +370,21 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
         }
     }
     if (e != hipSuccess) return hip_error(e, "host-to-device copy");
-    sllm_status st = launch();
+    const size_t obase = off;
+    void *o1[4];  // the usual case; more outputs take a vector
+    std::vector<void *> on(nout > 4 ? (size_t)nout : 0);
+    void **oaddr = nout > 4 ? on.data() : o1;
+    for (int i = 0; i < nout; i++) {
+        oaddr[i] = direct ? (void *)(hb + off) : out[i].dev;
+        off += (out[i].bytes + 255) & ~(size_t)255;
+    }
+    sllm_status st = launch((void *const *)oaddr);
     if (st != SLLM_OK) {
         (void)hipStreamSynchronize(c->stream);  // the inputs' copies still read the bounce buffer
         return st;
     }
-    const size_t obase = off;
-    for (int i = 0; i < nout && e == hipSuccess; i++) {
+    off = obase;
+    for (int i = 0; i < nout && e == hipSuccess && !direct; i++) {
         if (pin) {
             e = hipMemcpyAsync(hb + off, out[i].dev, out[i].bytes, hipMemcpyDeviceToHost, c->stream);
             off += (out[i].bytes + 255) & ~(size_t)255;
@@ -348,7 +392,7 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
             e = hipMemcpyAsync(out[i].dst, out[i].dev, out[i].bytes, hipMemcpyDeviceToHost, c->stream);
         }
     }
-    const hipError_t es = hipStreamSynchronize(c->stream);
+    const hipError_t es = wait_stream(c);
     if (e == hipSuccess) e = es;
     if (e != hipSuccess) return hip_error(e, "device-to-host copy");
     if (pin) {
@@ -862,7 +906,9 @@ sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *t
     int *dout = (int *)((char *)c->buf + ooff);
     const HostIn in{normed, dx, xb};
     const HostOut out{token, dout, sizeof(int)};
-    st = host_call(c, &in, 1, &out, 1, [&] { return sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, dout, c->stream); });
+    st = host_call(c, &in, 1, &out, 1, [&](void *const *o) {
+        return sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, (int *)o[0], c->stream);
+    });
     release(c);
     return st;
 }
@@ -921,8 +967,8 @@ sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *wg, const sllm_weight
     float *dh = (float *)((char *)c->buf + hoff);
     const HostIn in{x, dx, xb};
     const HostOut out{h, dh, hb};
-    st = host_call(c, &in, 1, &out, 1, [&] {
-        return sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, dh, nullptr, nullptr, c->stream);
+    st = host_call(c, &in, 1, &out, 1, [&](void *const *o) {
+        return sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, (float *)o[0], nullptr, nullptr, c->stream);
     });
     release(c);
     return st;
@@ -943,7 +989,8 @@ sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int
     float *dy = (float *)((char *)c->buf + yoff);
     const HostIn in{x, dx, xb};
     const HostOut out{dst, dy, yb};
-    st = host_call(c, &in, 1, &out, 1, [&] { return sllm_matmul_dev(w, dx, x_rows, x_cols, dy, c->stream); });
+    st = host_call(c, &in, 1, &out, 1,
+                   [&](void *const *o) { return sllm_matmul_dev(w, dx, x_rows, x_cols, (float *)o[0], c->stream); });
     release(c);
     return st;
 }
@@ -1029,7 +1076,8 @@ sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int c
         outs[(size_t)i] = HostOut{dst[i], dd[(size_t)i], (size_t)x_rows * ws[i]->rows * sizeof(float)};
     }
     const HostIn in{x, c->buf, xb};
-    st = host_call(c, &in, 1, outs.data(), count, [&] {
+    st = host_call(c, &in, 1, outs.data(), count, [&](void *const *o) {
+        for (int i = 0; i < count; i++) dd[(size_t)i] = (float *)o[i];
         return sllm_matmul_multi_dev(ws, count, (const float *)c->buf, x_rows, x_cols, dd.data(), c->stream);
     });
     release(c);

@@ -137,10 +137,23 @@ def _check(st: int) -> None:
         raise SllmError(st, msg.decode() if msg else "")
 
 
+def _flat_f32(a) -> np.ndarray:
+    """a as a 1-D C-contiguous float32 array (no copy when it already is one)."""
+    if type(a) is np.ndarray and a.dtype == np.float32 and a.ndim == 1 and a.flags.c_contiguous:
+        return a
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+
+
 def _ptr(a: np.ndarray) -> int:
-    if not a.flags["C_CONTIGUOUS"]:
+    """Address of a C-contiguous array's data (ctypes.addressof on a buffer view
+    costs a third of ndarray.ctypes.data; read-only or empty arrays take the
+    latter)."""
+    if not a.flags.c_contiguous:
         raise ValueError("array must be C-contiguous")
-    return a.ctypes.data
+    try:
+        return C.addressof(C.c_char.from_buffer(a))
+    except (TypeError, ValueError):
+        return a.ctypes.data
 
 
 def init() -> None:
@@ -247,7 +260,7 @@ def quantize_q8_rows_f32(flat: np.ndarray, rows: int, cols: int) -> DeviceWeight
 def model_matmul_quant_into_f32(w: DeviceWeight, x_data: np.ndarray, x_rows: int, x_cols: int,
                                 dst: np.ndarray | None = None):
     """float32_ops.go:379-460: returns (dst, xRows, Rows) like the Go function."""
-    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    x = _flat_f32(x_data)
     if x.size < x_rows * x_cols:
         raise SllmError(1, "xData shorter than xRows*xCols")
     n = x_rows * w.rows
@@ -259,7 +272,7 @@ def model_matmul_quant_into_f32(w: DeviceWeight, x_data: np.ndarray, x_rows: int
 
 def model_matmul_row_quant_into_f32(w: DeviceWeight, normed: np.ndarray, dst: np.ndarray | None = None):
     """float32_ops.go:620-707: one activation row."""
-    x = np.ascontiguousarray(normed, dtype=np.float32).reshape(-1)
+    x = _flat_f32(normed)
     if dst is None or dst.size < w.rows:
         dst = np.empty(w.rows, np.float32)
     _check(lib().sllm_matmul_row_quant_into_f32(w.handle, _ptr(x), _ptr(dst)))
@@ -276,7 +289,7 @@ def model_matmul_multi_quant_into_f32(ws: list, x_data: np.ndarray, x_rows: int,
     """Consecutive modelMatmulIntoF32 calls on one input (forwardBlock's q/k/v,
     model_f32.go:391-396, and gate/up, :479-482) in one call: returns one
     (x_rows * Rows) array per weight, as the single calls would."""
-    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    x = _flat_f32(x_data)
     if x.size < x_rows * x_cols:
         raise SllmError(1, "xData shorter than xRows*xCols")
     outs = [np.empty(x_rows * w.rows, np.float32) for w in ws]
@@ -297,7 +310,7 @@ def model_matmul_swiglu_into_f32(w_gate: DeviceWeight, w_up: DeviceWeight, x_dat
                                  x_cols: int) -> np.ndarray:
     """forwardBlock's gate / up matmuls and SwiGLU loop (model_f32.go:479-490) in
     one call: returns h (x_rows * Rows float32)."""
-    x = np.ascontiguousarray(x_data, dtype=np.float32).reshape(-1)
+    x = _flat_f32(x_data)
     if x.size < x_rows * x_cols:
         raise SllmError(1, "xData shorter than xRows*xCols")
     h = np.empty(x_rows * w_gate.rows, np.float32)
@@ -316,7 +329,7 @@ def matmul_swiglu_dev(w_gate: DeviceWeight, w_up: DeviceWeight, x_ptr: int, x_ro
 def matmul_argmax(w: DeviceWeight, normed: np.ndarray) -> int:
     """outputLogits' head matmul + argmaxF32 (greedy token) in one launch; only
     the index comes back to the host."""
-    x = np.ascontiguousarray(normed, dtype=np.float32).reshape(-1)
+    x = _flat_f32(normed)
     if x.size < w.cols:
         raise SllmError(1, "normed shorter than Cols")
     out = C.c_int()
