@@ -319,7 +319,15 @@ bool pinned(Ctx *c, size_t bytes) {
 // Past kSpinSeconds, or when the word cannot be used, the call blocks in
 // hipStreamSynchronize, which also reports a failed stream.
 hipError_t wait_stream(Ctx *c) {
-    if (!c->flag && hipHostMalloc((void **)&c->flag, 64, hipHostMallocCoherent) != hipSuccess) c->flag = nullptr;
+    if (!c->flag) {
+        if (hipHostMalloc((void **)&c->flag, 64, hipHostMallocCoherent) != hipSuccess) {
+            c->flag = nullptr;
+        } else {
+            // the allocation's contents are unspecified: start the sequence from a known value
+            __atomic_store_n(c->flag, 0u, __ATOMIC_RELEASE);
+            c->seq = 0;
+        }
+    }
     if (c->flag) {
         const unsigned want = ++c->seq;
         if (hipStreamWriteValue32(c->stream, c->flag, want, 0) == hipSuccess) {
