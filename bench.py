@@ -61,6 +61,8 @@ def main() -> int:
                     help="only launch the dominant GEMV and a 256 MiB copy (for rocprofv3 --pmc runs)")
     ap.add_argument("--gemm-probe", action="store_true",
                     help="only launch the prefill GEMMs (C3 / C4 shapes, M = 64 and 512) for rocprofv3 runs")
+    ap.add_argument("--valu-probe", action="store_true",
+                    help="only print the VALU issue rate of the instruction kinds the GEMV kernels use")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
@@ -83,6 +85,9 @@ def main() -> int:
         return traffic_probe(sq, synth, torch, stream, args.layers)
     if args.gemm_probe:
         return gemm_probe(sq, synth, torch, stream)
+    if args.valu_probe:
+        print(json.dumps({"valu_issue_rates": valu_rates()}), flush=True)
+        return 0
     print(f"[bench] building {args.layers} layer copies of C3 weights", file=sys.stderr, flush=True)
     gate_raw = synth.q4k_blocks(100, F, H)
     up_raw = synth.q4k_blocks(101, F, H)
@@ -341,6 +346,25 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
             r["dense_fp32_equiv_GBps"] = round(4.0 * N * K / (r["us"] * 1e-6) / 1e9, 1)
             table[f"{name} native {N}x{K} M=1"] = r
             del ws
+    # Q6_K streamed from its 6-bit codes (opt-in: tuning knob gemv_q6k_stream):
+    # the C3 down and the output head, the same weights timed streamed and from
+    # their Q8_0 planes (us_q8_planes)
+    sq.set_param("gemv_q6k_stream", 1)
+    try:
+        for N, K, seed in ((H, F, 102), (128256, H, 204)):
+            raw = synth.q6k_blocks(seed, N, K)
+            w0 = sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K)
+            n = int(min(64, max(2, -(-ROTATE_BYTES // w0.plane_bytes))))
+            ws = [w0] + [sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K) for _ in range(n - 1)]
+            r = run(ws, 1, 100)
+            sq.set_param("gemv_q6k_stream", 0)
+            rq = run(ws, 1, 100)
+            sq.set_param("gemv_q6k_stream", 1)
+            r.update({"us_q8_planes": rq["us"], "fp64_blocks": ws[0].q6k_exact_blocks})
+            table[f"q6k streamed {N}x{K} M=1 (opt-in)"] = r
+            del ws
+    finally:
+        sq.set_param("gemv_q6k_stream", 0)
     torch.cuda.empty_cache()
     return table
 
@@ -723,6 +747,28 @@ def mfma_peaks() -> dict | None:
             out[name] = round(t.value, 1)
     out["note"] = ("4096 workgroups x 4 waves, 8 independent MFMA chains per wave, register operands only; the "
                    "fastest of 5 launches")
+    return out
+
+
+VALU_KINDS = ["v_fma_f32", "v_mul_f32", "v_add_u32", "v_lshrrev_b32", "v_cvt_f32_ubyte1", "v_cvt_i32_f32",
+              "v_perm_b32", "v_dot4_i32_i8", "v_bfe_u32", "v_and_or_b32", "v_mad_i32_i24"]
+
+
+def valu_rates() -> dict | None:
+    """VALU issue rate, T lane-instructions per second, of each instruction kind
+    in VALU_KINDS on the box, from libsllm_probe.so (eight independent chains
+    per lane on register operands, 2048 workgroups x 4 waves, fastest of 5)."""
+    import ctypes as C
+    path = os.path.join(ROOT, "scriptling-llm-lib_amd", "libsllm_probe.so")
+    if not os.path.exists(path):
+        return None
+    L = C.CDLL(path)
+    L.sllm_probe_valu_rate.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
+    out = {}
+    for op, name in enumerate(VALU_KINDS):
+        t = C.c_double()
+        if L.sllm_probe_valu_rate(op, 2048, 1024, 5, C.byref(t)) == 0:
+            out[name] = round(t.value, 1)
     return out
 
 

@@ -135,6 +135,19 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
 sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes);
 
 /*
+ * GGUF Q6_K weights loaded while the tuning knob "gemv_q6k_stream" is set
+ * keep their 6-bit codes beside the Q8_0 planes (28.25 B per 32 weights,
+ * against 34), and while the knob is set the decode GEMV streams those and
+ * rebuilds the Q8_0 codes and scale in registers, bit-identical to the Q8_0
+ * planes the reference's load computes (dequantizeQ6KBlock + quantizeQ8Rows,
+ * gguf.go:988-1015, 1080-1134). *blocks: the 32-element blocks it recomputes
+ * with the reference's fp64 arithmetic (where the fast per-sub-block rule
+ * cannot reproduce the rounding of exact ties), or -1 for a weight loaded
+ * without those planes. No counterpart in the reference.
+ */
+sllm_status sllm_weight_q6k_exact_blocks(const sllm_weight *w, int64_t *blocks);
+
+/*
  * Rebuild the reference Raw bytes (QuantWeight.Raw layout) from the device
  * planes into host memory (cap >= raw_bytes). Bit-exact inverse of the repack.
  * SLLM_Q2K / SLLM_Q3K: the GGUF super-block bytes the weight was made from.
@@ -376,6 +389,8 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
  *   gemv_max_nb         1..8       most 32-element blocks per lane per unit (8)
  *   gemv_inflight_kb    >= 64      weight bytes in flight over the device (32768)
  *   gemv_q4k_stream     0, 1       Q4_K weights streamed from their own headers (0)
+ *   gemv_q6k_stream     0, 1       Q6_K weights loaded with, and streamed from, their
+ *                                  6-bit codes (0; see sllm_weight_q6k_exact_blocks)
  *   gemm_min_rows       >= 1       activation rows from which the GEMM is used (64;
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)

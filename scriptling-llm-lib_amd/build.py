@@ -14,7 +14,7 @@ PROBE_LIB = os.path.join(HERE, "libsllm_probe.so")
 PROBE_SOURCE = "probe_mfma.hip"
 
 SOURCES = ["qmm_api.hip", "qmm_gemv.hip", "qmm_gemv_q8.hip", "qmm_gemv_q4.hip", "qmm_gemv_q4_1.hip",
-           "qmm_gemv_q5.hip", "qmm_gemv_q5k1.hip", "qmm_gemv_q4k.hip", "qmm_gemv_q2k.hip", "qmm_gemv_q3k.hip", "qmm_gemm.hip", "qmm_pack.hip", "qmm_attn.hip"]
+           "qmm_gemv_q5.hip", "qmm_gemv_q5k1.hip", "qmm_gemv_q4k.hip", "qmm_gemv_q6k.hip", "qmm_gemv_q2k.hip", "qmm_gemv_q3k.hip", "qmm_gemm.hip", "qmm_pack.hip", "qmm_attn.hip"]
 
 # -ffp-contract=off: every float operation rounds separately, as in the reference.
 # -packed-fp32-ops off: no v_pk_*_f32 in the device code.

@@ -1,5 +1,6 @@
-// Peak-rate probe of the int8 matrix cores (measurement only; bench.py loads
-// libsllm_probe.so, the library never does). Every wave runs chains of
+// Peak-rate probes (measurement only; bench.py loads libsllm_probe.so, the
+// library never does): the int8 matrix cores, and the VALU issue rate of the
+// instruction kinds the GEMV kernels use. Every wave of the MFMA probe runs chains of
 // independent int8 MFMAs on register operands - no memory traffic inside the
 // loop - and writes its accumulators once, so the launch time is the matrix
 // cores' issue rate:
@@ -45,9 +46,88 @@ __global__ void __launch_bounds__(256) mfma_loop(v4i *out, int iters, int seed) 
     out[blockIdx.x * blockDim.x + threadIdx.x] = t;
 }
 
+// VALU issue rate of one instruction kind: eight independent chains per lane
+// (each result feeds the next instruction of its chain only), register
+// operands, no memory traffic inside the loop.
+#define SLLM_PROBE_CHAINS(ASM)                                          \
+    _Pragma("unroll") for (int i = 0; i < 8; i++) asm volatile(ASM : "+v"(r[i]) : "v"(c1), "v"(c2));
+
+template <int OP>
+__global__ void __launch_bounds__(256) valu_loop(unsigned *out, int iters, unsigned seed) {
+    unsigned r[8];
+    const unsigned c1 = seed * 3u + threadIdx.x, c2 = seed ^ 0x0c0c0400u;
+#pragma unroll
+    for (int i = 0; i < 8; i++) r[i] = threadIdx.x * 77u + i;
+    for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            if (OP == 0) { SLLM_PROBE_CHAINS("v_fma_f32 %0, %0, %1, %2") }
+            else if (OP == 1) { SLLM_PROBE_CHAINS("v_mul_f32 %0, %0, %1") }
+            else if (OP == 2) { SLLM_PROBE_CHAINS("v_add_u32 %0, %0, %1") }
+            else if (OP == 3) { SLLM_PROBE_CHAINS("v_lshrrev_b32 %0, %1, %0") }
+            else if (OP == 4) { SLLM_PROBE_CHAINS("v_cvt_f32_ubyte1 %0, %0") }
+            else if (OP == 5) { SLLM_PROBE_CHAINS("v_cvt_i32_f32 %0, %0") }
+            else if (OP == 6) { SLLM_PROBE_CHAINS("v_perm_b32 %0, %0, %1, %2") }
+            else if (OP == 7) { SLLM_PROBE_CHAINS("v_dot4_i32_i8 %0, %1, %2, %0") }
+            else if (OP == 8) { SLLM_PROBE_CHAINS("v_bfe_u32 %0, %0, %1, %2") }
+            else if (OP == 9) { SLLM_PROBE_CHAINS("v_and_or_b32 %0, %0, %1, %2") }
+            else { SLLM_PROBE_CHAINS("v_mad_i32_i24 %0, %0, %1, %2") }
+        }
+    }
+    unsigned t = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) t ^= r[i];
+    out[blockIdx.x * blockDim.x + threadIdx.x] = t;
+}
+#undef SLLM_PROBE_CHAINS
+
 }  // namespace
 
 extern "C" {
+
+// Issue rate of VALU instruction kind `op` (0 v_fma_f32, 1 v_mul_f32,
+// 2 v_add_u32, 3 v_lshrrev_b32, 4 v_cvt_f32_ubyte1, 5 v_cvt_i32_f32,
+// 6 v_perm_b32, 7 v_dot4_i32_i8, 8 v_bfe_u32, 9 v_and_or_b32,
+// 10 v_mad_i32_i24) in T lane-instructions per second, the fastest of `reps`
+// launches of `blocks` workgroups of 4 waves. Returns 0 or a hipError_t.
+int sllm_probe_valu_rate(int op, int blocks, int iters, int reps, double *rate) {
+    if (!rate || blocks <= 0 || iters <= 0 || reps <= 0 || op < 0 || op > 10) return (int)hipErrorInvalidValue;
+    unsigned *out = nullptr;
+    hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(unsigned));
+    if (e != hipSuccess) return (int)e;
+    hipEvent_t a, b;
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    float best = 0.0f;
+    for (int r = 0; r <= reps && e == hipSuccess; r++) {  // launch 0 warms up
+        (void)hipEventRecord(a, nullptr);
+        switch (op) {
+        case 0: hipLaunchKernelGGL(valu_loop<0>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 1: hipLaunchKernelGGL(valu_loop<1>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 2: hipLaunchKernelGGL(valu_loop<2>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 3: hipLaunchKernelGGL(valu_loop<3>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 4: hipLaunchKernelGGL(valu_loop<4>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 5: hipLaunchKernelGGL(valu_loop<5>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 6: hipLaunchKernelGGL(valu_loop<6>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 7: hipLaunchKernelGGL(valu_loop<7>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 8: hipLaunchKernelGGL(valu_loop<8>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        case 9: hipLaunchKernelGGL(valu_loop<9>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        default: hipLaunchKernelGGL(valu_loop<10>, dim3(blocks), dim3(256), 0, nullptr, out, iters, (unsigned)r); break;
+        }
+        e = hipGetLastError();
+        (void)hipEventRecord(b, nullptr);
+        if (e == hipSuccess) e = hipEventSynchronize(b);
+        float ms = 0.0f;
+        if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+        if (e == hipSuccess && r > 0 && (best == 0.0f || ms < best)) best = ms;
+    }
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    (void)hipFree(out);
+    if (e != hipSuccess) return (int)e;
+    *rate = (double)blocks * 256 * iters * 16 * 8 / (best * 1e-3) / 1e12;
+    return 0;
+}
 
 // Runs `reps` launches of form `form` (0 or 1) over `blocks` workgroups of 4
 // waves, `iters` loop trips each, on the current device's null stream, and

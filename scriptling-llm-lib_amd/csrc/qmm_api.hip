@@ -15,7 +15,9 @@
 
 struct sllm_weight {
     int fmt = 0;     // the QType at the ABI
-    int layout = 0;  // the plane layout (SLLM_Q4K_STREAM: Q4_1 planes + the Q4_K headers)
+    int layout = 0;  // the plane layout (SLLM_Q4K_STREAM: Q4_1 planes + the Q4_K headers;
+                     // SLLM_Q6K_STREAM: Q8_0 planes + the streamed Q6_K planes)
+    int64_t q6_exceptions = 0;  // SLLM_Q6K_STREAM: blocks the GEMV recomputes in fp64
     int groups = 0, rows = 0, cols = 0;
     int device = 0;
     void *base = nullptr;
@@ -434,9 +436,12 @@ bool uses_gemm(const sllm_weight *w, int x_rows) {
 }
 
 // The GEMV kernel format of a weight: Q4_K weights stream their GGUF headers
-// (unless the tuning knob says otherwise), every other weight its QType's planes.
+// and Q6_K weights loaded with their native planes stream those, while the
+// tuning knob of each says so; every other weight its QType's planes.
 int gemv_fmt(const sllm_weight *w) {
-    return (w->layout == SLLM_Q4K_STREAM && tuning().gemv_q4k_stream) ? SLLM_Q4K_STREAM : w->fmt;
+    if (w->layout == SLLM_Q4K_STREAM && tuning().gemv_q4k_stream) return SLLM_Q4K_STREAM;
+    if (w->layout == SLLM_Q6K_STREAM && tuning().gemv_q6k_stream) return SLLM_Q6K_STREAM;
+    return w->fmt;
 }
 
 // One weight's matmul on device buffers: the GEMV, or the GEMM with the given
@@ -690,6 +695,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemm_splits") && value >= 0 && value <= 64) t.gemm_splits = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
+    else if (!std::strcmp(name, "gemv_q6k_stream") && (value == 0 || value == 1)) t.gemv_q6k_stream = value;
     else return set_error(SLLM_ERR_ARG, std::string("unknown parameter or value: ") + name);
     return SLLM_OK;
 }
@@ -750,7 +756,10 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     case 6: fmt = SLLM_Q5_0; per = 22; break;
     case 12: fmt = SLLM_Q4_1; per = 144; blk = 256; layout = SLLM_Q4K_STREAM; break;
     case 13: fmt = SLLM_Q5K1; per = 176; blk = 256; break;
-    case 14: fmt = SLLM_Q8_0; per = 210; blk = 256; break;
+    case 14:
+        fmt = SLLM_Q8_0; per = 210; blk = 256;
+        if (tuning().gemv_q6k_stream) layout = SLLM_Q6K_STREAM;
+        break;
     case 20: fmt = SLLM_Q8_0; per = 18; break;
     case 10: fmt = SLLM_Q2K; per = 84; blk = 256; break;
     case 11: fmt = SLLM_Q3K; per = 110; blk = 256; break;
@@ -764,11 +773,20 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     if ((st = ensure_init()) != SLLM_OK) return st;
     sllm_weight *w = nullptr;
     if ((st = alloc_weight(fmt, rows, cols, &w, layout)) != SLLM_OK) return st;
+    uint32_t q6stat[2] = {0, 0};
     st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
         const uint8_t *dev = (const uint8_t *)c->buf;
         if (t == 8 || t == 2 || t == 3 || t == 6) return pack_from_raw(fmt, dev, rows, cols / 32, w->planes, nullptr, c->stream);
-        return pack_from_gguf(t, dev, rows, cols, w->planes, c->stream);
+        if (w->layout != SLLM_Q6K_STREAM) return pack_from_gguf(t, dev, rows, cols, w->planes, c->stream);
+        SLLM_HIP(hipMemsetAsync(w->planes.q6stat, 0, sizeof(q6stat), c->stream));
+        sllm_status ps = pack_q6k_stream(dev, rows, cols, w->planes, c->stream);
+        if (ps != SLLM_OK) return ps;
+        SLLM_HIP(hipMemcpyAsync(q6stat, w->planes.q6stat, sizeof(q6stat), hipMemcpyDeviceToHost, c->stream));
+        return SLLM_OK;
     });
+    if (st == SLLM_OK && q6stat[1] != 0)
+        st = set_error(SLLM_ERR_DEVICE, "Q6_K stream pack: the fp64 requantization disagrees with the Q8_0 planes");
+    w->q6_exceptions = q6stat[0];
     if (st != SLLM_OK) {
         sllm_weight_destroy(w);
         return st;
@@ -816,6 +834,12 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
 sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes) {
     if (!w || !bytes) return set_error(SLLM_ERR_ARG, "null pointer");
     *bytes = stream_bytes_of(gemv_fmt(w), (int64_t)w->rows * w->groups);
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_q6k_exact_blocks(const sllm_weight *w, int64_t *blocks) {
+    if (!w || !blocks) return set_error(SLLM_ERR_ARG, "null pointer");
+    *blocks = w->layout == SLLM_Q6K_STREAM ? w->q6_exceptions : -1;
     return SLLM_OK;
 }
 

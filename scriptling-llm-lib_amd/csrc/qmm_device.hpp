@@ -56,6 +56,12 @@ __device__ __forceinline__ uint16_t f32_to_f16_trunc(float f) {
     return (uint16_t)(sign | ((uint32_t)e16 << 10) | ((u >> 13) & 0x3ffu));
 }
 
+// Go's byte(int8(f64)) on amd64 (CVTTSD2SL, low byte): NaN -> 0.
+__device__ __forceinline__ uint32_t f64_to_i8_byte(double v) {
+    if (!(v >= -2147483648.0 && v < 2147483648.0)) return 0;
+    return (uint32_t)(int8_t)(int32_t)v & 0xffu;
+}
+
 // f16_exact(f32_to_f16_trunc(f)) without the round trip: the f16 normal range
 // keeps the top 10 mantissa bits, below it a signed zero, above it a signed
 // Inf, NaN / Inf give +0.

@@ -33,6 +33,10 @@ extern template sllm_status launch_mt<SLLM_Q4K_STREAM, false>(int, int, int, con
                                                                 int, int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q4K_STREAM, true>(int, int, int, const SegTable &, const float *, int, int,
                                                                int, int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q6K_STREAM, false>(int, int, int, const SegTable &, const float *, int, int,
+                                                                int, int, int, int, size_t, hipStream_t);
+extern template sllm_status launch_mt<SLLM_Q6K_STREAM, true>(int, int, int, const SegTable &, const float *, int, int,
+                                                               int, int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q2K, false>(int, int, int, const SegTable &, const float *, int, int, int,
                                                          int, int, int, size_t, hipStream_t);
 extern template sllm_status launch_mt<SLLM_Q2K, true>(int, int, int, const SegTable &, const float *, int, int, int,
@@ -106,7 +110,11 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     const int lg = (G + 63) / 64;
     // Q5_0 reads 32 fp32 activations per block from LDS: more than two blocks
     // per lane per unit only adds registers (measured: 3 % slower at NB 7)
-    const int nb_cap = fmt == SLLM_Q5_0 && T.gemv_max_nb > 2 ? 2 : T.gemv_max_nb;
+    // Q6_K streamed: one block per lane per unit - its requantization holds
+    // about 40 registers per block, and with several blocks of one unit
+    // interleaved the GEMV spills (the ring's depth D still covers the latency)
+    int nb_cap = fmt == SLLM_Q5_0 && T.gemv_max_nb > 2 ? 2 : T.gemv_max_nb;
+    if (fmt == SLLM_Q6K_STREAM) nb_cap = 1;
     int NB = lg;
     if (lg > nb_cap) {
         NB = nb_cap;
@@ -175,6 +183,7 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         case SLLM_Q5_0: st = SLLM_GEMV_FMT(SLLM_Q5_0); break;
         case SLLM_Q5K1: st = SLLM_GEMV_FMT(SLLM_Q5K1); break;
         case SLLM_Q4K_STREAM: st = SLLM_GEMV_FMT(SLLM_Q4K_STREAM); break;
+        case SLLM_Q6K_STREAM: st = SLLM_GEMV_FMT(SLLM_Q6K_STREAM); break;
         case SLLM_Q2K: st = SLLM_GEMV_FMT(SLLM_Q2K); break;
         case SLLM_Q3K: st = SLLM_GEMV_FMT(SLLM_Q3K); break;
         default: return set_error(SLLM_ERR_QTYPE, "gemv: unknown format");

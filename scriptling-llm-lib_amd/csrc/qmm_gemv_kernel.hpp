@@ -26,6 +26,7 @@
 
 #include "qmm_device.hpp"
 #include "qmm_internal.hpp"
+#include "qmm_q6k.hpp"
 
 namespace sllm {
 namespace gemv {
@@ -109,11 +110,13 @@ struct BlockRegs {
     int4 q, q2;
     uint16_t d, m, dh;
     uint32_t qh;
-    uint2 c2;      // native k-quants: the 2-bit codes
+    uint2 c2;      // native k-quants: the 2-bit codes; Q6_K streamed: the top code bits
     uint32_t sbw;  // native k-quants: the super-block's scale word
     int4 hq;       // Q4_K streamed: the super-block's GGUF header
     uint32_t jj;   // Q4_K streamed: the block's index in its super-block
 };
+// Q6_K streamed uses q (low nibbles), c2 (top bits), qh (the m6 word) and d
+// (the super-block's d).
 
 template <class T>
 __device__ __forceinline__ const T *at(const T *base, uint32_t idx) {
@@ -128,6 +131,13 @@ __device__ __forceinline__ void load_block(const Planes &P, uint32_t idx, BlockR
         b.d = ld_nt(at(P.d, idx));
         b.sbw = ld_nt(at(P.sb, idx >> 3));  // rows hold whole super-blocks (G % 8 == 0)
         if (FMT == SLLM_Q3K) b.qh = ld_nt(at(P.qh, idx));
+        return;
+    }
+    if (FMT == SLLM_Q6K_STREAM) {
+        b.q = ld_nt(at(P.l6, idx));
+        b.c2 = ld_nt(at(P.h6, idx));
+        b.qh = ld_nt(at(P.m6, idx));
+        b.d = ld_nt(at(P.d6, idx >> 3));  // rows hold whole super-blocks (G % 8 == 0)
         return;
     }
     b.q = ld_nt(at(P.qs, idx));
@@ -614,6 +624,25 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
 
     // the terms of one block (all MT activation rows)
     auto block_terms = [&](const BlockRegs &b, int g, int i) {
+        if constexpr (FMT == SLLM_Q6K_STREAM) {
+            // the Q8_0 codes and scale, rebuilt once for every activation row,
+            // then the Q8_0 term (q8q8.go:187-195 + vnni_amd64.s:70-73)
+            int4 wl, wh;
+            float sv;
+            q6s::requant(b.q, b.c2, b.qh, b.d, wl, wh, sv);
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                if (m >= M) continue;
+                ActRegs xa;
+                if (HOIST) xa = xh[HOIST ? i : 0][HOIST ? m : 0];
+                else load_act<FMT>(A, (size_t)m * G + g, xa);
+                const int isum = q8_isum(wl, wh, xa.xl, xa.xh);
+                const float cmb = sv * xa.xs;
+                const float term = cmb * (float)isum;
+                acc[m] = acc[m] + term;
+            }
+            return;
+        }
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             if (m >= M) continue;

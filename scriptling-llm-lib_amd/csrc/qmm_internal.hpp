@@ -30,6 +30,10 @@ namespace sllm {
 //   sb   u32 per super-block: Q2K d | dmin << 16, Q3K d (f16 bits)
 //   hdr  16 B per super-block (Q4_K streamed natively): the GGUF Q4_K header
 //        (d, dmin, the 12 packed scale bytes), next to the Q4_1 planes
+// Q6_K streamed natively (SLLM_Q6K_STREAM), next to the Q8_0 planes: l6 / h6
+// the 6-bit codes (16 + 8 B), m6 the block's scales, code maximum and flags,
+// d6 the super-block's f16 d (qmm_q6k.hpp has the layout); q6stat two
+// counters the pack fills: blocks left to the fp64 path, self-check failures.
 struct Planes {
     const int4 *qs = nullptr;
     const int4 *qs2 = nullptr;
@@ -40,6 +44,10 @@ struct Planes {
     const uint2 *q2 = nullptr;
     const uint32_t *sb = nullptr;
     const int4 *hdr = nullptr;
+    const int4 *l6 = nullptr;
+    const uint2 *h6 = nullptr;
+    const uint32_t *m6 = nullptr;
+    const uint16_t *d6 = nullptr;
 };
 
 struct MutPlanes {
@@ -52,6 +60,11 @@ struct MutPlanes {
     uint2 *q2 = nullptr;
     uint32_t *sb = nullptr;
     int4 *hdr = nullptr;
+    int4 *l6 = nullptr;
+    uint2 *h6 = nullptr;
+    uint32_t *m6 = nullptr;
+    uint16_t *d6 = nullptr;
+    uint32_t *q6stat = nullptr;
 };
 
 // Kernel format of a Q4_K weight streamed natively: the Q4_1 nibble plane plus
@@ -60,6 +73,11 @@ struct MutPlanes {
 // Internal only: such a weight is a "q4_1" QuantWeight at the ABI (its d / m
 // planes serve the GEMM and the export).
 constexpr int SLLM_Q4K_STREAM = 7;
+// Kernel format of a Q6_K weight streamed natively: the 6-bit codes and the
+// per-block scale data, the Q8_0 codes rebuilt in registers (qmm_q6k.hpp).
+// Internal only: such a weight is a "q8" QuantWeight at the ABI, and its Q8_0
+// planes, kept beside the stream's, serve the GEMM and the export.
+constexpr int SLLM_Q6K_STREAM = 8;
 
 // Formats whose activations stay fp32 (no Q8_0 codes): Q5_0 and the native k-quants.
 __host__ __device__ constexpr bool act_f32(int fmt) {
@@ -77,6 +95,7 @@ inline int plane_block_bytes(int fmt) {
     case SLLM_Q5_0: return 22;
     case SLLM_Q5K1: return 26;
     case SLLM_Q4K_STREAM: return 18;  // 16 + 16 / 8
+    case SLLM_Q6K_STREAM: return 29;  // 28.25: 16 + 8 + 4 + 2 / 8 (rounded up)
     case SLLM_Q2K: return 11;  // 10.5: 8 + 2 + 4 / 8 (rounded up)
     case SLLM_Q3K: return 15;  // 14.5: 8 + 4 + 2 + 4 / 8 (rounded up)
     }
@@ -88,6 +107,7 @@ inline size_t stream_bytes_of(int fmt, int64_t nb) {
     if (fmt == SLLM_Q2K) return (size_t)nb * 10 + (size_t)(nb / 8) * 4;
     if (fmt == SLLM_Q3K) return (size_t)nb * 14 + (size_t)(nb / 8) * 4;
     if (fmt == SLLM_Q4K_STREAM) return (size_t)nb * 16 + (size_t)(nb / 8) * 16;
+    if (fmt == SLLM_Q6K_STREAM) return (size_t)nb * 28 + (size_t)(nb / 8) * 2;
     return (size_t)nb * plane_block_bytes(fmt);
 }
 
@@ -130,6 +150,7 @@ inline Planes as_const(const MutPlanes &p) {
     Planes c;
     c.qs = p.qs; c.qs2 = p.qs2; c.d = p.d; c.m = p.m; c.dh = p.dh; c.qh = p.qh;
     c.q2 = p.q2; c.sb = p.sb; c.hdr = p.hdr;
+    c.l6 = p.l6; c.h6 = p.h6; c.m6 = p.m6; c.d6 = p.d6;
     return c;
 }
 
@@ -195,6 +216,9 @@ sllm_status pack_from_raw(int fmt, const uint8_t *raw_dev, int rows, int G, cons
 sllm_status pack_from_gguf(uint32_t ggml_type, const uint8_t *raw_dev, int rows, int cols,
                            const MutPlanes &P, hipStream_t s);
 sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
+// GGUF Q6_K -> the Q8_0 planes and the streamed Q6_K planes (P.q6stat zeroed
+// by the caller; the pack counts into it).
+sllm_status pack_q6k_stream(const uint8_t *raw_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
 // GGUF super-block bytes of a native k-quant weight from its (host copy of the) planes.
 void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *out);
 
@@ -234,6 +258,7 @@ struct Tuning {
     int gemm_wn = 0;           // GEMM waves along N per workgroup / 2 (1, 2, 4; 0: by tile count)
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
+    int gemv_q6k_stream = 0;   // Q6_K weights: load (and stream) the native 6-bit planes (1) or the Q8_0 planes only (0)
     int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
     int attn_tile_groups = 4;      // attention: most tile groups (of max(4, rep) waves) per workgroup
     int attn_head_slices = 0;      // attention: workgroups sharing one kv head's q heads (0: by workgroup count)

@@ -16,6 +16,7 @@
 
 #include "qmm_device.hpp"
 #include "qmm_internal.hpp"
+#include "qmm_q6k.hpp"
 
 namespace sllm {
 
@@ -41,7 +42,17 @@ size_t carve_planes(int fmt, int64_t nb, void *base, MutPlanes *out) {
         return (off + 255) & ~(size_t)255;
     }
     p.qs = (int4 *)take(n * 16);
-    if (fmt == SLLM_Q8_0) p.qs2 = (int4 *)take(n * 16);
+    if (fmt == SLLM_Q8_0 || fmt == SLLM_Q6K_STREAM) p.qs2 = (int4 *)take(n * 16);
+    if (fmt == SLLM_Q6K_STREAM) {
+        p.d = (uint16_t *)take(n * 2);
+        p.l6 = (int4 *)take(n * 16);
+        p.h6 = (uint2 *)take(n * 8);
+        p.m6 = (uint32_t *)take(n * 4);
+        p.d6 = (uint16_t *)take(n / 8 * 2);
+        p.q6stat = (uint32_t *)take(2 * sizeof(uint32_t));
+        if (out) *out = p;
+        return (off + 255) & ~(size_t)255;
+    }
     if (fmt == SLLM_Q5_0 || fmt == SLLM_Q5K1) p.qh = (uint32_t *)take(n * 4);
     p.d = (uint16_t *)take(n * 2);
     if (fmt == SLLM_Q4_1 || fmt == SLLM_Q5K1 || fmt == SLLM_Q4K_STREAM) p.m = (uint16_t *)take(n * 2);
@@ -66,12 +77,6 @@ __device__ __forceinline__ int4 ld_int4(const uint8_t *p) {
     return v;
 }
 __device__ __forceinline__ double f16_to_f64(uint16_t h) { return (double)f16_exact(h); }
-
-// Go's byte(int8(f64)) on amd64 (CVTTSD2SL, low byte): NaN -> 0.
-__device__ __forceinline__ uint32_t f64_to_i8_byte(double v) {
-    if (!(v >= -2147483648.0 && v < 2147483648.0)) return 0;
-    return (uint32_t)(int8_t)(int32_t)v & 0xffu;
-}
 
 // quantizeQ8Rows (gguf.go:1098-1125) for one block of 32 fp64 values.
 __device__ void q8_from_f64(const double *v, int4 &lo, int4 &hi, uint16_t &d) {
@@ -234,6 +239,89 @@ __global__ void pack_q6k_kernel(const uint8_t *__restrict__ raw, int64_t nb, Mut
         P.qs[b] = lo;
         P.qs2[b] = hi;
         P.d[b] = dd;
+    }
+}
+
+// Q6_K (210 B / 256) -> the Q8_0 planes (as pack_q6k_kernel) and the streamed
+// Q6_K planes (qmm_q6k.hpp). Per block: the 6-bit codes, Mi = max |sc q|, and
+// per sub-block the direction the reference rounded its ties in - a tie is an
+// element with 127 |sc q| / Mi = k + 1/2 exactly, i.e. 254 |sc q| an odd
+// multiple of Mi, and it went toward zero when its Q8_0 code is k. Then the
+// GEMV's rule is evaluated on the stored planes and compared with the Q8_0
+// codes and scale: a block where they differ gets the X bit (the GEMV redoes
+// it in fp64) and is counted in q6stat[0]; a block where the GEMV's fp64 path
+// differs would be a defect and is counted in q6stat[1] (the load then fails).
+__global__ void pack_q6k_stream_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x) {
+        const uint8_t *sb = raw + (b >> 3) * 210;
+        const int j = (int)(b & 7), n = j >> 2, k = j & 3;
+        const uint16_t dbits = ld16(sb + 208);
+        const double d = f16_to_f64(dbits);
+        const uint8_t *ql = sb + n * 64 + (k & 1) * 32;
+        const uint8_t *qh = sb + 128 + n * 32;
+        const uint8_t *sc = sb + 192 + n * 8 + 2 * k;
+        const int s[2] = {(int)(int8_t)sc[0], (int)(int8_t)sc[1]};
+        int u[32];
+        double v[32];
+        int mi = 0;
+        for (int l = 0; l < 32; l++) {
+            const int nib = (k < 2) ? (ql[l] & 0x0f) : (ql[l] >> 4);
+            u[l] = nib | (((qh[l] >> (2 * k)) & 3) << 4);
+            const int q = u[l] - 32;
+            v[l] = d * (double)s[l / 16] * (double)q;
+            const int a = s[l / 16] * q < 0 ? -(s[l / 16] * q) : s[l / 16] * q;
+            mi = a > mi ? a : mi;
+        }
+        int4 lo, hi;
+        uint16_t dd;
+        q8_from_f64(v, lo, hi, dd);
+        P.qs[b] = lo;
+        P.qs2[b] = hi;
+        P.d[b] = dd;
+
+        const uint32_t cw[8] = {(uint32_t)lo.x, (uint32_t)lo.y, (uint32_t)lo.z, (uint32_t)lo.w,
+                                (uint32_t)hi.x, (uint32_t)hi.y, (uint32_t)hi.z, (uint32_t)hi.w};
+        uint32_t l6[4] = {0, 0, 0, 0}, h6[2] = {0, 0}, dec = 0;
+        for (int e = 0; e < 32; e++) {
+            const int jw = (e & 15) >> 2, i = e & 3;  // word jw, byte i of its half
+            l6[jw] |= (uint32_t)(u[e] & 15) << (8 * i + (e >= 16 ? 4 : 0));
+            h6[e >> 4] |= (uint32_t)(u[e] >> 4) << (8 * i + 2 * jw);
+            const int sq = s[e / 16] * (u[e] - 32);
+            const int a = sq < 0 ? -sq : sq;
+            if (mi > 0 && (254 * a) % mi == 0 && ((254 * a / mi) & 1)) {
+                const int c = (int)(int8_t)((cw[e >> 2] >> (8 * (e & 3))) & 0xffu);
+                if ((c < 0 ? -c : c) == (254 * a / mi - 1) / 2) dec |= 1u << (e / 16);
+            }
+        }
+        const bool finite_nonzero = (dbits & 0x7fffu) != 0 && (dbits & 0x7c00u) != 0x7c00u;
+        uint32_t m6 = (uint32_t)(s[0] & 0xff) | ((uint32_t)(s[1] & 0xff) << 8) |
+                      ((uint32_t)(finite_nonzero ? mi : 0) << 16) | (dec << 29);
+        const int4 l6v = make_int4((int)l6[0], (int)l6[1], (int)l6[2], (int)l6[3]);
+        const uint2 h6v = make_uint2(h6[0], h6[1]);
+        uint32_t uu[8];
+        q6s::unpack(l6v, h6v, uu);
+        const float ref_sv = f16_lut(dd);
+        int4 flo, fhi;
+        q6s::codes_fast(uu, m6, dbits, flo, fhi);
+        const float fsv = q6s::scale_fast(m6, dbits);
+        const bool fast_ok = flo.x == lo.x && flo.y == lo.y && flo.z == lo.z && flo.w == lo.w && fhi.x == hi.x &&
+                             fhi.y == hi.y && fhi.z == hi.z && fhi.w == hi.w &&
+                             __float_as_uint(fsv) == __float_as_uint(ref_sv);
+        if (!fast_ok) {
+            m6 |= 1u << 31;
+            atomicAdd(&P.q6stat[0], 1u);
+        }
+        int4 elo, ehi;
+        float esv;
+        q6s::codes_exact(l6v, h6v, m6, dbits, elo, ehi, esv);
+        const bool exact_ok = elo.x == lo.x && elo.y == lo.y && elo.z == lo.z && elo.w == lo.w && ehi.x == hi.x &&
+                              ehi.y == hi.y && ehi.z == hi.z && ehi.w == hi.w &&
+                              __float_as_uint(esv) == __float_as_uint(ref_sv);
+        if (!exact_ok) atomicAdd(&P.q6stat[1], 1u);
+        P.l6[b] = l6v;
+        P.h6[b] = h6v;
+        P.m6[b] = m6;
+        if (j == 0) P.d6[b >> 3] = dbits;
     }
 }
 
@@ -407,6 +495,13 @@ void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *o) {
             sb[109] = (uint8_t)((p.sb[s] >> 8) & 0xff);
         }
     }
+}
+
+sllm_status pack_q6k_stream(const uint8_t *raw_dev, int rows, int cols, const MutPlanes &P, hipStream_t s) {
+    const int64_t nb = (int64_t)rows * (cols / 32);
+    hipLaunchKernelGGL(pack_q6k_stream_kernel, dim3(grid_for(nb)), dim3(256), 0, s, raw_dev, nb, P);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
 }
 
 sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlanes &P, hipStream_t s) {

@@ -104,6 +104,7 @@ def lib() -> C.CDLL:
     L.sllm_set_param.argtypes = [C.c_char_p, i32]
     L.sllm_matmul_add_dev.argtypes = [W, P, i32, i32, P, P]
     L.sllm_weight_stream_bytes.argtypes = [W, C.POINTER(sz)]
+    L.sllm_weight_q6k_exact_blocks.argtypes = [W, C.POINTER(C.c_int64)]
     L.sllm_kv_cache_create.argtypes = [i32, i32, i32, i32, C.POINTER(P)]
     L.sllm_kv_cache_destroy.argtypes = [P]
     L.sllm_kv_cache_length.argtypes = [P, i32, C.POINTER(i32)]
@@ -200,6 +201,14 @@ class DeviceWeight:
         """Bytes one GEMV streams from this weight's planes (sllm_weight_stream_bytes)."""
         n = C.c_size_t()
         _check(lib().sllm_weight_stream_bytes(self.handle, C.byref(n)))
+        return n.value
+
+    @property
+    def q6k_exact_blocks(self) -> int:
+        """Q6_K streamed: blocks the GEMV recomputes in fp64; -1 without the
+        streamed planes (sllm_weight_q6k_exact_blocks)."""
+        n = C.c_int64()
+        _check(lib().sllm_weight_q6k_exact_blocks(self.handle, C.byref(n)))
         return n.value
 
     @classmethod
