@@ -186,7 +186,7 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x_dev, int x_rows
  * Equivalent to count calls of sllm_matmul_quant_into_f32 (dst[i] receives
  * x_rows x Rows(ws[i]) floats, bit-identical to the single call's result),
  * but decode GEMVs of weights with the same QType share one launch (up to
- * four weights each) and x is uploaded once. Every ws[i] must have
+ * four weights each) and x is staged once. Every ws[i] must have
  * Cols == x_cols.
  */
 sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int count, const float *x,

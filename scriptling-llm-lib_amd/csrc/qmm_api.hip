@@ -69,6 +69,9 @@ constexpr size_t kMaxPinnedBytes = (size_t)64 << 20;
 // straight into the pinned buffer (device-visible host memory), without a
 // device-to-host copy.
 constexpr size_t kDirectOutBytes = (size_t)1 << 20;
+// Inputs of at most this size are read by the kernels from the pinned bounce
+// buffer (no upload enqueue); larger ones are uploaded first.
+constexpr size_t kDirectInBytes = (size_t)64 << 10;
 // How long a call spins on its completion word before it blocks in
 // hipStreamSynchronize instead (long calls, or a stream in error).
 constexpr double kSpinSeconds = 2e-3;
@@ -347,9 +350,10 @@ hipError_t wait_stream(Ctx *c) {
 
 // One host-buffer call: copy the inputs (host -> device staging), run
 // `launch` on the context's stream, bring the outputs back and wait for the
-// stream. Small transfers bounce through pinned memory; small outputs are
-// written by the kernels into the pinned buffer itself. launch(oaddr) gets
-// the device-visible address each output is to be written to.
+// stream. Small transfers bounce through pinned memory; small inputs are read
+// by the kernels from the pinned buffer itself (no upload enqueue) and small
+// outputs are written there. launch(iaddr, oaddr) gets the device-visible
+// address each input is to be read from and each output is to be written to.
 struct HostIn {
     const void *src;
     void *dev;
@@ -366,14 +370,20 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
     for (int i = 0; i < nin; i++) tin += (in[i].bytes + 255) & ~(size_t)255;
     for (int i = 0; i < nout; i++) tout += (out[i].bytes + 255) & ~(size_t)255;
     const bool pin = pinned(c, tin + tout);
+    const bool direct_in = pin && tin <= kDirectInBytes;
     const bool direct = pin && tout <= kDirectOutBytes;
     char *hb = (char *)c->hbuf;
     hipError_t e = hipSuccess;
     size_t off = 0;
+    void *i1[4];
+    std::vector<void *> inv(nin > 4 ? (size_t)nin : 0);
+    void **iaddr = nin > 4 ? inv.data() : i1;
     for (int i = 0; i < nin && e == hipSuccess; i++) {
+        iaddr[i] = in[i].dev;
         if (pin) {
             std::memcpy(hb + off, in[i].src, in[i].bytes);
-            e = hipMemcpyAsync(in[i].dev, hb + off, in[i].bytes, hipMemcpyHostToDevice, c->stream);
+            if (direct_in) iaddr[i] = hb + off;
+            else e = hipMemcpyAsync(in[i].dev, hb + off, in[i].bytes, hipMemcpyHostToDevice, c->stream);
             off += (in[i].bytes + 255) & ~(size_t)255;
         } else {
             e = hipMemcpyAsync(in[i].dev, in[i].src, in[i].bytes, hipMemcpyHostToDevice, c->stream);
@@ -388,9 +398,9 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
         oaddr[i] = direct ? (void *)(hb + off) : out[i].dev;
         off += (out[i].bytes + 255) & ~(size_t)255;
     }
-    sllm_status st = launch((void *const *)oaddr);
+    sllm_status st = launch((void *const *)iaddr, (void *const *)oaddr);
     if (st != SLLM_OK) {
-        (void)hipStreamSynchronize(c->stream);  // the inputs' copies still read the bounce buffer
+        (void)hipStreamSynchronize(c->stream);  // the inputs' copies or kernels still read the bounce buffer
         return st;
     }
     off = obase;
@@ -938,8 +948,8 @@ sllm_status sllm_matmul_argmax(const sllm_weight *w, const float *normed, int *t
     int *dout = (int *)((char *)c->buf + ooff);
     const HostIn in{normed, dx, xb};
     const HostOut out{token, dout, sizeof(int)};
-    st = host_call(c, &in, 1, &out, 1, [&](void *const *o) {
-        return sllm_matmul_argmax_dev(w, dx, w->cols, nullptr, (int *)o[0], c->stream);
+    st = host_call(c, &in, 1, &out, 1, [&](void *const *i, void *const *o) {
+        return sllm_matmul_argmax_dev(w, (const float *)i[0], w->cols, nullptr, (int *)o[0], c->stream);
     });
     release(c);
     return st;
@@ -999,8 +1009,9 @@ sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *wg, const sllm_weight
     float *dh = (float *)((char *)c->buf + hoff);
     const HostIn in{x, dx, xb};
     const HostOut out{h, dh, hb};
-    st = host_call(c, &in, 1, &out, 1, [&](void *const *o) {
-        return sllm_matmul_swiglu_dev(wg, wu, dx, x_rows, x_cols, (float *)o[0], nullptr, nullptr, c->stream);
+    st = host_call(c, &in, 1, &out, 1, [&](void *const *i, void *const *o) {
+        return sllm_matmul_swiglu_dev(wg, wu, (const float *)i[0], x_rows, x_cols, (float *)o[0], nullptr, nullptr,
+                                      c->stream);
     });
     release(c);
     return st;
@@ -1021,8 +1032,9 @@ sllm_status sllm_matmul_quant_into_f32(const sllm_weight *w, const float *x, int
     float *dy = (float *)((char *)c->buf + yoff);
     const HostIn in{x, dx, xb};
     const HostOut out{dst, dy, yb};
-    st = host_call(c, &in, 1, &out, 1,
-                   [&](void *const *o) { return sllm_matmul_dev(w, dx, x_rows, x_cols, (float *)o[0], c->stream); });
+    st = host_call(c, &in, 1, &out, 1, [&](void *const *i, void *const *o) {
+        return sllm_matmul_dev(w, (const float *)i[0], x_rows, x_cols, (float *)o[0], c->stream);
+    });
     release(c);
     return st;
 }
@@ -1108,9 +1120,9 @@ sllm_status sllm_matmul_multi_quant_into_f32(const sllm_weight *const *ws, int c
         outs[(size_t)i] = HostOut{dst[i], dd[(size_t)i], (size_t)x_rows * ws[i]->rows * sizeof(float)};
     }
     const HostIn in{x, c->buf, xb};
-    st = host_call(c, &in, 1, outs.data(), count, [&](void *const *o) {
+    st = host_call(c, &in, 1, outs.data(), count, [&](void *const *xi, void *const *o) {
         for (int i = 0; i < count; i++) dd[(size_t)i] = (float *)o[i];
-        return sllm_matmul_multi_dev(ws, count, (const float *)c->buf, x_rows, x_cols, dd.data(), c->stream);
+        return sllm_matmul_multi_dev(ws, count, (const float *)xi[0], x_rows, x_cols, dd.data(), c->stream);
     });
     release(c);
     return st;
