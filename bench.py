@@ -255,6 +255,33 @@ def time_launches(torch, stream, launch, n: int, warm: int = 10, trials: int = 1
             "launches_per_trial": n}
 
 
+def graph_launch_us(torch, stream, launch, n: int, replays: int = 10) -> float:
+    """Per-launch time (us) of n calls launch(i, stream) captured into one HIP
+    graph on a side stream and replayed on `stream` (median of `replays`)."""
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        for i in range(2):
+            launch(i, cs.cuda_stream)
+    cs.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for i in range(n):
+            launch(i, cs.cuda_stream)
+    g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(replays):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        g.replay()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ts.append(a.elapsed_time(b) / n * 1e3)
+    del g
+    return sorted(ts)[len(ts) // 2]
+
+
 def config_table(sq, synth, torch, stream, peaks=None) -> dict:
     """The kernels of BASELINE configs C1, C2, C4 (and C3 at prefill sizes).
 
@@ -265,7 +292,9 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
     on the box (the K = 64 form; the published 5.0 POPS when the probe did not
     run), or for Q5_0 (fp32 activations, exact per-block sums on the VALU at 2
     ops per MAC) against the 78.6 T lane-ops/s VALU peak. Q5_K rows stream 26 B / 32 weights (the two Q4_1 halves of
-    convertQ5KToTwoQ41 without the high half's zero mins and 4-bit codes)."""
+    convertQ5KToTwoQ41 without the high half's zero mins and 4-bit codes).
+    M = 1 lines also give us_graph: the per-launch time of 100 of the same
+    calls replayed from one HIP graph (C1-sized GEMVs are launch-bound)."""
     import numpy as np
     H, F, KV = 4096, 14336, 1024
     sp = stream.cuda_stream
@@ -292,6 +321,12 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
         r = {"us": round(us, 2), "us_median": round(st["median"], 2), "us_min": round(st["min"], 2),
              "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
              "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if M == 1:
+            # launch-bound shapes: the same calls replayed from one HIP graph
+            # (n launches, rotating copies), the per-launch cost without the
+            # host's enqueue path
+            r["us_graph"] = round(graph_launch_us(torch, stream, lambda i, s_: sq.matmul_dev(
+                ws[i % len(ws)], xin.data_ptr(), M, K, out.data_ptr(), s_), 100), 2)
         if M >= 64:
             tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
             if ws[0].qtype == "q5":
