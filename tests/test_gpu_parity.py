@@ -216,3 +216,25 @@ def test_errors_are_status_codes():
     with pytest.raises(sq.SllmError) as e:
         sq.DeviceWeight.from_quant(sq.QuantWeight("q9", raw, 2, 4, 64))
     assert e.value.status == 2
+
+
+@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1"])
+@pytest.mark.parametrize("Ns", [(10001,), (5000, 5001), (17003,), (9000, 4100, 3)])
+def test_row_orders_with_partial_and_spare_waves(qtype, Ns):
+    # rows per wave = ceil(total rows / 4096 wave slots): 3 (10001 rows) and
+    # 5 (17003 rows) take consecutive rows per wave, 4 (13103 rows) strided
+    # ones; a partly filled last wave per weight, spare waves that own no row,
+    # and several weights sharing one launch (q/k/v-style segments)
+    K = 256
+    ws, raws = [], []
+    for i, N in enumerate(Ns):
+        raw = make_raw(qtype, N, K, seed=N + i)
+        raws.append(raw)
+        ws.append(sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K)))
+    x = make_x(1, K, seed=len(Ns))
+    outs = sq.model_matmul_multi_quant_into_f32(ws, x, 1, K)
+    for N, raw, got in zip(Ns, raws, outs):
+        ref = oracle.matmul(qtype, raw, N, x)
+        assert_fp32_parity(got.reshape(1, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} {Ns} N={N}")
+        single, _, _ = sq.model_matmul_quant_into_f32(ws[Ns.index(N)], x, 1, K)
+        assert np.array_equal(single.view(np.uint32), got.view(np.uint32))
