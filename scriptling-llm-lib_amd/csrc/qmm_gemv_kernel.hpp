@@ -595,6 +595,17 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
         load_unit<FMT, NB>(lup ? P2 : P, u, base);
     };
 
+    // The residual add (o / down): each lane's dst value is loaded before
+    // anything else, so the add at the end does not wait a memory round trip
+    // (dst is only written there).
+    float pre[MT];
+#pragma unroll
+    for (int m = 0; m < MT; m++) {
+        pre[m] = 0.0f;
+        if (!PAIR && S.accum && m < M && lane < real_rows) pre[m] = dst[(size_t)m * N + base + lane * step];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     BlockRegs buf[D][NB];
     // Prologue: the activation rows (M x G blocks) are quantized by all
     // threads, TPB lanes per block. Each thread issues its activation loads
@@ -737,7 +748,7 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
                 if (S.dst[2]) S.dst[2][o] = u;
             } else if (dst) {
                 // model_f32.go:472-474 / 495-497: x[i] += o[i], one float32 add
-                dst[o] = S.accum ? dst[o] + res[m] : res[m];
+                dst[o] = S.accum ? pre[m] + res[m] : res[m];
             }
         }
     }
