@@ -91,3 +91,36 @@ def test_swiglu_errors():
     with pytest.raises(sq.SllmError) as e:
         sq.model_matmul_swiglu_into_f32(a, b, x, 1, 64)     # Rows differ
     assert e.value.status == 1
+
+
+@pytest.mark.parametrize("N", [9000, 12001, 14336])
+def test_paired_row_orders(N):
+    # pairs per wave = ceil(N / 4096 wave slots): 3 for 9000 and 12001 rows
+    # (consecutive rows per wave, a partly filled last wave, spare waves), 4
+    # for 14336 (strided rows); with and without the RMSNorm prologue
+    K = 256
+    _, wg = _w("q4_1", N, K, seed=N)
+    _, wu = _w("q4_1", N, K, seed=N + 1)
+    x = make_x(1, K, seed=N % 97)
+    xd = torch.from_numpy(x).cuda()
+    nw = torch.from_numpy(np.random.default_rng(N).normal(1, 0.1, K).astype(np.float32)).cuda()
+    s = torch.cuda.current_stream().cuda_stream
+    h = torch.empty(N, device="cuda")
+    gt = torch.empty(N, device="cuda")
+    up = torch.empty(N, device="cuda")
+    sq.matmul_swiglu_dev(wg, wu, xd.data_ptr(), 1, K, h.data_ptr(), gt.data_ptr(), up.data_ptr(), s)
+    g1 = torch.empty(N, device="cuda")
+    u1 = torch.empty(N, device="cuda")
+    sq.matmul_multi_dev([wg, wu], xd.data_ptr(), 1, K, [g1.data_ptr(), u1.data_ptr()], s)
+    hn = torch.empty(N, device="cuda")
+    sq.rmsnorm_matmul_swiglu_dev(wg, wu, xd.data_ptr(), nw.data_ptr(), 1e-5, 1, K, hn.data_ptr(), s)
+    gn = torch.empty(N, device="cuda")
+    un = torch.empty(N, device="cuda")
+    sq.rmsnorm_matmul_multi_dev([wg, wu], xd.data_ptr(), nw.data_ptr(), 1e-5, 1, K, [gn.data_ptr(), un.data_ptr()], s)
+    torch.cuda.synchronize()
+    assert torch.equal(gt.view(torch.int32), g1.view(torch.int32))
+    assert torch.equal(up.view(torch.int32), u1.view(torch.int32))
+    want = oracle.swiglu(gt.cpu().numpy(), up.cpu().numpy())
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
+    wantn = oracle.swiglu(gn.cpu().numpy(), un.cpu().numpy())
+    assert np.array_equal(hn.cpu().numpy().view(np.uint32), wantn.view(np.uint32))
