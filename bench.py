@@ -66,7 +66,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
-              "Each GPU would own a slice of the weight rows; see the sharding note in DESIGN.md.",
+              "Each GPU would own a slice of the weight rows (its dst rows) and read the whole activation row.",
               file=sys.stderr)
         return 2
 
