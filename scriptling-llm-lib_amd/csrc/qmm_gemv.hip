@@ -164,6 +164,14 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         const int64_t inflight = (int64_t)T.gemv_inflight_kb * 1024;
         int D = 1;
         while (D * 2 * NB * MT <= 8 && D * 2 <= U && waves * unit_bytes * D * 2 <= inflight) D *= 2;
+        // the RMSNorm prologue is longer than the plain one: a launch whose
+        // waves stream many units keeps two in flight, so that more weight
+        // bytes arrive while the row statistics are formed. Measured (rotating
+        // copies, two boxes): RMSNorm + head + argmax (Q8_0 128256x4096, 32
+        // rows per wave) 85.4-86.4 µs against 86.3-87.2 with one unit; the
+        // plain head is faster with one (84.0 against 86.9), and RMSNorm +
+        // gate/up + SwiGLU slower with four (16.0 against 15.1 with two)
+        if (norm_w && D == 1 && U >= 16 && 2 * NB * MT <= 8) D = 2;
         const int mrows = left < MT ? left : MT;
         const size_t lds = act_lds_bytes(fmt, MT, G);
         const float *xp = x + (size_t)done * G * 32;
