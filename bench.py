@@ -558,6 +558,13 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
 
     full = decode_full_step(sq, torch, stream, layer_ws, head, nw, eps, xh, tokens)
 
+    # the per-token head launch alone (RMSNorm + head + greedy argmax; its
+    # 558 MB do not fit the MALL, so back-to-back launches read HBM)
+    sp = stream.cuda_stream
+    hst = time_launches(torch, stream, lambda i: sq.rmsnorm_matmul_argmax_dev(head, P(xh), P(nw), eps, P(tok), 0, sp),
+                        20, trials=5)
+    head_us = {k: round(hst[k], 2) for k in ("mean", "median", "min")}
+
     # The drop-in path as the Go binding would drive it: host buffers in and
     # out of every call (x uploaded, dst downloaded, synchronous), with the
     # host-side multi-weight and SwiGLU entries: 129 calls per token.
@@ -580,7 +587,8 @@ def decode_tok_s(sq, synth, torch, stream, tokens: int) -> dict:
     ms_host = (time.time() - t0) / nh * 1e3
     del layer_ws, head
     torch.cuda.empty_cache()
-    return {**full, "decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
+    return {**full, "rmsnorm_head_argmax_us": head_us,
+            "decode_gemv_tok_s": round(1e3 / ms, 1), "decode_gemv_ms_per_token": round(ms, 4),
             "decode_gemv_tok_s_without_norms": round(1e3 / ms_plain, 1),
             "decode_gemv_tok_s_graph": round(1e3 / ms_graph, 1),
             "decode_gemv_ms_per_token_graph": round(ms_graph, 4),
