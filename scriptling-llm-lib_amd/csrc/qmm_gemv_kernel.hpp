@@ -208,7 +208,9 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
 #pragma unroll
             for (int l = 0; l < 16; l++) {
                 const float q = (float)((w >> (2 * l)) & 3u);
-                const float wt = dl * q - ml;
+                // dl * q is exact (at most 17 significant bits), so one fused
+                // multiply-add rounds the difference exactly as mul + sub does
+                const float wt = __builtin_fmaf(dl, q, -ml);
                 sum = sum + elem(x.xf, 16 * h + l) * wt;
             }
         }
