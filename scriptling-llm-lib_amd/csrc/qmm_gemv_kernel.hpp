@@ -205,9 +205,19 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
             const uint32_t sc = ((uint32_t)b.d >> (8 * h)) & 0xffu;
             const float dl = d * (float)(sc & 0xfu), ml = dm * (float)(sc >> 4);
             const uint32_t w = h ? b.c2.y : b.c2.x;
+            // codes l, l+4, l+8, l+12 as the bytes of sp[l & 3]: each converts
+            // with one byte-to-float instruction (no per-code bit extract; the
+            // empty asm keeps the compiler from folding the masks back into
+            // one extract per code)
+            uint32_t sp[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                sp[j] = (w >> (2 * j)) & 0x03030303u;
+                asm volatile("" : "+v"(sp[j]));
+            }
 #pragma unroll
             for (int l = 0; l < 16; l++) {
-                const float q = (float)((w >> (2 * l)) & 3u);
+                const float q = (float)((sp[l & 3] >> (8 * (l >> 2))) & 0xffu);
                 // dl * q is exact (at most 17 significant bits), so one fused
                 // multiply-add rounds the difference exactly as mul + sub does
                 const float wt = __builtin_fmaf(dl, q, -ml);
