@@ -234,13 +234,43 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const float dl = d * (float)(int)(int8_t)(((uint32_t)b.d >> (8 * h)) & 0xffu);
+            const float ndl4 = -4.0f * dl;
             const uint32_t w = h ? b.c2.y : b.c2.x;
-            const uint32_t hb = b.qh >> (16 * h);
+            const uint32_t hb = b.qh >> (16 * h);  // 0: subtract 4
+            // q + 4 = code + 4 * (high bit), in 0..7, for elements l, l+4,
+            // l+8, l+12 as the bytes of sp[l & 3] (the high bits moved from
+            // stride 4 to bit 2 of each byte), each converted with one
+            // byte-to-float instruction; the empty asm keeps the compiler from
+            // folding the masks back into one extract per element
+            uint32_t sp[4];
 #pragma unroll
-            for (int l = 0; l < 16; l++) {
-                const int q = (int)((w >> (2 * l)) & 3u) - (((hb >> l) & 1u) ? 0 : 4);
-                const float wt = dl * (float)q;
-                sum = sum + elem(x.xf, 16 * h + l) * wt;
+            for (int j = 0; j < 4; j++) {
+                uint32_t t = (hb >> j) & 0x1111u;                   // bits 0, 4, 8, 12
+                t = (t & 0x0011u) | ((t & 0x1100u) << 8);           // bits 0, 4, 16, 20
+                t = (t & 0x00010001u) | ((t & 0x00100010u) << 4);   // bits 0, 8, 16, 24
+                sp[j] = ((w >> (2 * j)) & 0x03030303u) | (t << 2);
+                asm volatile("" : "+v"(sp[j]));
+            }
+            if (__all(__builtin_isfinite(dl))) {
+#pragma unroll
+                for (int l = 0; l < 16; l++) {
+                    const float q4 = (float)((sp[l & 3] >> (8 * (l >> 2))) & 0xffu);
+                    // dl * (q + 4) is exact (at most 20 significant bits) and so
+                    // is dl * q, so one fused multiply-add gives dl * q exactly
+                    // (a zero as +0 where dl * q can be -0: the sum starts at +0
+                    // and, rounded to nearest, is never -0, so adding either zero
+                    // leaves it). An infinite dl would make it inf - inf: waves
+                    // holding one take the plain product below.
+                    const float wt = __builtin_fmaf(dl, q4, ndl4);
+                    sum = sum + elem(x.xf, 16 * h + l) * wt;
+                }
+            } else {
+#pragma unroll
+                for (int l = 0; l < 16; l++) {
+                    const float q = (float)((sp[l & 3] >> (8 * (l >> 2))) & 0xffu) - 4.0f;
+                    const float wt = dl * q;
+                    sum = sum + elem(x.xf, 16 * h + l) * wt;
+                }
             }
         }
         acc = acc + sum;

@@ -66,6 +66,31 @@ def test_block_sums_bit_exact(t):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("t", [10, 11])
+def test_block_sums_bit_exact_special_scales(t):
+    # super-block scales d (and Q2_K's dmin) of +-inf, NaN, +-0 and the
+    # smallest f16 subnormal among ordinary ones: the rebuilt weights follow
+    # IEEE rules as the reference's fp64 dequantization rounded to float32 does
+    N, K, M = 24, 768, 2
+    raw = make_kq(t, N, K, 4).reshape(-1, PER[t])
+    special = [0x7C00, 0xFC00, 0x7E00, 0x0000, 0x8000, 0x0001, 0x8001]
+    at = 80 if t == 10 else 108
+    for i, bits in enumerate(special):
+        raw[3 * i, at:at + 2] = [bits & 0xFF, bits >> 8]
+        if t == 10:
+            raw[3 * i + 1, 82:84] = [bits & 0xFF, bits >> 8]
+    raw = raw.reshape(-1)
+    w = sq.load_weight_f32_direct(t, raw, N, K)
+    W = oracle.dense_weights(t, raw, N, K)
+    x = make_x(M, K, seed=5)
+    got = sq.debug_block_dots(w, x).view(np.float32)
+    want = oracle.dense_block_sums(W, x)
+    gn, wn = np.isnan(got), np.isnan(want)
+    assert np.array_equal(gn, wn)
+    assert gn.any()  # the infinite and NaN scales were reached
+    assert np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
+
+
 @pytest.mark.parametrize("t,N,K,M", [(10, 300, 4096, 1), (11, 300, 4096, 1), (10, 96, 2048, 3),
                                      (11, 64, 1024, 70), (10, 14336, 4096, 1), (11, 4096, 14336, 1)])
 def test_matmul_within_reassociation_bound(t, N, K, M):
