@@ -324,11 +324,13 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
         t = t * x.xs;
         acc = acc + t;
         if (FMT == SLLM_Q5K1) {
-            // high Q4_1 block of convertQ5KToTwoQ41: scale dh, min +0, 0/1 codes
+            // high Q4_1 block of convertQ5KToTwoQ41: scale dh, min +0, 0/1 codes.
+            // Its min term float(Σxq) * +0 is a zero, and adding it changes h1
+            // only from -0 to +0; acc2 starts at +0 and, rounded to nearest, is
+            // never -0, so adding either zero leaves it - the term is left out,
+            // as in the GEMM (bit-identical)
             const int hsum = bits_isum(b.qh, x.xl, x.xh);
-            const float h1 = (float)hsum * f16_exact(b.dh);
-            const float h2 = fsx * 0.0f;
-            float h = h1 + h2;
+            float h = (float)hsum * f16_exact(b.dh);
             h = h * x.xs;
             acc2 = acc2 + h;
         }
