@@ -230,14 +230,16 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
         float4 b = xb[jj + 4];  // elements 16+4jj ..
         const float av[4] = {a.x, a.y, a.z, a.w};
         const float bv[4] = {b.x, b.y, b.z, b.w};
-        // the four codes of elements 4jj+k (lo) and 16+4jj+k (hi) as bytes k,
-        // so each converts with one byte-to-float instruction
-        const uint32_t lo = (w[jj] & 0x0f0f0f0fu) | ((uint32_t)spread4(qh >> (4 * jj)) << 4);
-        const uint32_t hi = ((w[jj] >> 4) & 0x0f0f0f0fu) | ((uint32_t)spread4(qh >> (16 + 4 * jj)) << 4);
+        // q5 - 16 of elements 4jj+k (lo) and 16+4jj+k (hi) as signed bytes k:
+        // the nibble, with 0xf0 above it where the high bit is clear (the
+        // nibble - 16), so each converts with one sign-extending byte-to-float
+        // instruction; float(q5 - 16) is float(q5) - 16 exactly (+0 for 16)
+        const uint32_t lo = (w[jj] & 0x0f0f0f0fu) | ((uint32_t)spread4(~qh >> (4 * jj)) * 0xf0u);
+        const uint32_t hi = ((w[jj] >> 4) & 0x0f0f0f0fu) | ((uint32_t)spread4(~qh >> (16 + 4 * jj)) * 0xf0u);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            float v0 = (float)((lo >> (8 * k)) & 0xffu) - 16.0f;
-            float v1 = (float)((hi >> (8 * k)) & 0xffu) - 16.0f;
+            float v0 = (float)(int)(int8_t)((lo >> (8 * k)) & 0xffu);
+            float v1 = (float)(int)(int8_t)((hi >> (8 * k)) & 0xffu);
             float p0 = v0 * av[k];
             float p1 = v1 * bv[k];
             float pair = p0 + p1;
