@@ -380,6 +380,21 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
                                   int32_t *out);
 
 /*
+ * The prefill GEMM's own block dots: runs the int8 matrix-core GEMM (the
+ * kernel sllm_matmul uses from gemm_min_rows activation rows on) on x_rows
+ * (>= 1) rows against weight rows [row0, row0 + n_rows), and writes every
+ * int32 block dot its MFMA instructions returned, from the registers its
+ * epilogue scales: out int32 [x_rows][n_rows][groups] (x2 for Q5K1: low,
+ * high). Q4_0 entries include the -8 Σxq zero-point term, as
+ * sllm_debug_block_dots. Formats Q8_0, Q4_0, Q4_1, Q5K1 (cols a multiple of
+ * 64); others SLLM_ERR_QTYPE. Replaces no reference interface: the
+ * reference forms the same per-(row, block) dots in q8q8.go:156-195,
+ * q4q8.go:58-77 and q41q8.go:31-52.
+ */
+sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int x_rows, int x_cols,
+                                       int row0, int n_rows, int32_t *out);
+
+/*
  * Launch-shape knobs (no counterpart in the reference: its matmuls have no
  * launch shapes). Process-wide; set them before the calls they should
  * affect, not while other threads are launching. Results do not depend on
@@ -394,7 +409,9 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
  *   gemm_min_rows       >= 1       activation rows from which the GEMM is used (64;
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)
- *   gemm_wn             0, 1, 2, 4 GEMM waves along N / 2 per workgroup (0: by tile count)
+ *   gemm_shape          0, 1, 2    GEMM workgroup tiles: 1 = 64 x 128, 2 = 64 x 64 with each
+ *                                  K stage split over two waves (0: 2 for Q5K1, else 1;
+ *                                  the shape moves the fp32 summation splits)
  *   gemm_splits         0..64      GEMM K splits, added in split order (0: by tile count;
  *                                  the split count moves the fp32 summation splits)
  *   attn_target_blocks  1..65536   attention: about this many workgroups when splitting (512)

@@ -701,7 +701,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "attn_tile_groups") && value >= 1 && value <= 4) t.attn_tile_groups = value;
     else if (!std::strcmp(name, "attn_head_slices") && value >= 0 && value <= 64) t.attn_head_slices = value;
-    else if (!std::strcmp(name, "gemm_wn") && (value == 0 || value == 1 || value == 2 || value == 4)) t.gemm_wn = value;
+    else if (!std::strcmp(name, "gemm_shape") && value >= 0 && value <= 2) t.gemm_shape = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemm_splits") && value >= 0 && value <= 64) t.gemm_splits = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
@@ -1199,6 +1199,49 @@ sllm_status sllm_debug_block_dots(const sllm_weight *w, const float *x, int x_ro
     }
     release(c);
     if (e != hipSuccess) return hip_error(e, "debug_block_dots");
+    return st;
+}
+
+sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int x_rows, int x_cols, int row0,
+                                       int n_rows, int32_t *out) {
+    if (!w || !x || !out) return set_error(SLLM_ERR_ARG, "null pointer");
+    if (x_rows <= 0 || x_cols != w->cols) return set_error(SLLM_ERR_ARG, "bad activation shape");
+    if (row0 < 0 || n_rows <= 0 || row0 > w->rows - n_rows) return set_error(SLLM_ERR_ARG, "bad weight row range");
+    if (w->fmt != SLLM_Q8_0 && w->fmt != SLLM_Q4_0 && w->fmt != SLLM_Q4_1 && w->fmt != SLLM_Q5K1)
+        return set_error(SLLM_ERR_QTYPE, "gemm block dots: the format has no int8 GEMM");
+    if (!gemm_supported(w->fmt, w->groups)) return set_error(SLLM_ERR_SHAPE, "gemm block dots: cols not supported");
+    sllm_status st = ensure_init();
+    if (st != SLLM_OK) return st;
+    // the weight rows [row0, row0 + n_rows) as a weight of their own: every plane is [rows][groups]
+    Planes P = as_const(w->planes);
+    const size_t off = (size_t)row0 * w->groups;
+    P.qs += off;
+    if (P.qs2) P.qs2 += off;
+    P.d += off;
+    if (P.m) P.m += off;
+    if (P.dh) P.dh += off;
+    if (P.qh) P.qh += off;
+    const int G = w->groups;
+    const size_t xb = align256((size_t)x_rows * x_cols * 4);
+    const size_t gb = align256(gemm_workspace_bytes(w->fmt, n_rows, G, x_rows));
+    const size_t db = align256((size_t)x_rows * n_rows * 4);
+    const size_t ob = (size_t)x_rows * n_rows * G * 4 * (w->fmt == SLLM_Q5K1 ? 2 : 1);
+    Ctx *c = nullptr;
+    if ((st = acquire(&c, xb + gb + db + ob)) != SLLM_OK) return st;
+    char *b = (char *)c->buf;
+    hipError_t e = hipMemcpyAsync(b, x, (size_t)x_rows * x_cols * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        st = launch_gemm_dots(w->fmt, P, (const float *)b, (float *)(b + xb + gb), n_rows, G, x_rows, b + xb, gb,
+                              (int32_t *)(b + xb + gb + db), c->stream);
+        if (st == SLLM_OK) {
+            e = hipMemcpyAsync(out, b + xb + gb + db, ob, hipMemcpyDeviceToHost, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        } else {
+            (void)hipStreamSynchronize(c->stream);
+        }
+    }
+    release(c);
+    if (e != hipSuccess) return hip_error(e, "debug_gemm_block_dots");
     return st;
 }
 

@@ -3,25 +3,44 @@
 //
 // 1. The activation rows are quantized once into a workspace (xq int8 [M][K],
 //    xs fp32 [M][G], Σxq int32 [M][G]) by the GEMV prologue's routine.
-// 2. A workgroup of 2 x WN waves computes a 64 x BN tile of dst (64
-//    activation rows x BN = 32 WN weight rows), each wave a 32 x 32 sub-tile.
-//    K is staged KB blocks at a time through LDS, double-buffered: the global
-//    loads of stage s+1 are in flight while stage s is computed. Per 32-element
-//    block each wave runs v_mfma_i32_16x16x32_i8 on its four 16 x 16 pieces:
-//    K = 32 is exactly one block, so every MFMA returns exact int32 block dots
-//    (the reference's isum / qsum). The epilogue forms the reference's
-//    per-block fp32 term from them, exactly as the GEMV does, and accumulates.
-// 3. When there are too few tiles to fill the device, K is split over S
+// 2. A workgroup of WM x WN x WK waves computes a (32 WM) x (64 WN) tile of
+//    dst; each wave a 32 x 64 sub-tile (two 32 x 32 MFMA tiles) over every
+//    WK-th block of each K stage, the WK partial tiles added at the end in a
+//    fixed tree order. K is staged KB blocks at a time through LDS,
+//    double-buffered: the global loads of stage s+1 are in flight while stage
+//    s is computed.
+// 3. Per 32-element block a wave issues v_mfma_i32_32x32x32_i8 per 32 x 32
+//    tile: K = 32 is exactly one block, so every result is one block's exact
+//    int32 dot (the reference's isum / qsum). Its C operand is the int32 bit
+//    pattern of 1.5 * 2^23 (Q4_0: minus 8 Σxq, q4q8.go:66-77), so each result
+//    is the bit pattern of the float 1.5 * 2^23 + dot (exact: |dot| < 2^22):
+//    the epilogue needs no int-to-float conversion.
+// 4. The epilogue scales each block dot by its weight and activation scales
+//    with fused multiply-adds, in the arrangement of the reference's arm64
+//    kernels (q4q8_row_arm64.s, q41q8_row_arm64.s:59-63: per-lane FMLA
+//    accumulators added at the end):
+//      t   = fma(F, d, -1.5 * 2^23 * d)   = round(dot * d)  (exact addend)
+//      Q4_1 / Q5K1: t = fma(float(Σxq), m, t)              (min term)
+//      Q5K1: t = t + round(dot_high * d_high)               (high block)
+//      acc = fma(t, xs, acc)
+//    Each per-block term is rounded at most twice fewer times than in the
+//    reference's x86 order (cmb = d * xs, term = cmb * float(dot), acc += term),
+//    so every output differs from the reference's sequential sum by a few
+//    ulp of sum |term| at most; the tests hold it to 1e-5 * sum |term|.
+//    A K stage whose weight scales are not finite, or whose activation scales
+//    reach 2^90 (where d * xs could overflow while dot * d does not), is
+//    computed in the reference's exact operation order instead: the choice is
+//    one per workgroup and stage (any thread that stores such a scale tags the
+//    stage in LDS), and it keeps the reference's Inf / NaN results.
+// 5. When there are too few tiles to fill the device, K is also split over S
 //    workgroups; each writes its partial tile and a second kernel adds the S
 //    partials in split order (fixed order: results are reproducible).
 //
-// MFMA operand layout (16x16x32 i8): A[i][k] in lane i + 16 (k / 8), byte
-// k % 8; B[k][j] in lane j + 16 (k / 8); D[i][j] in lane j + 16 (i / 4),
-// element i % 4.
-//
-// Roofline: the per-block fp32 epilogue (4-6 VALU ops per output per 32 MACs)
-// bounds this kernel, not the matrix cores (which it keeps about 10 % busy) or,
-// from M ~ 64 up, HBM.
+// MFMA operand layout (32x32x32 i8): A row i in lanes i and i + 32, 16 bytes
+// each; B column j in lanes j and j + 32; D[i][j] in lane j + 32 h, element
+// 4 q + r for i = 8 q + 4 h + r. A block's 32 codes are stored in LDS in the
+// order (0..7, 16..23, 8..15, 24..31), so lane half h reads its 16 bytes with
+// one ds_read_b128 and both operands pair the same elements.
 #include <hip/hip_runtime.h>
 
 #include "qmm_device.hpp"
@@ -32,102 +51,73 @@ namespace sllm {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
-constexpr int kBM = 64;   // activation rows per workgroup
-constexpr int kKB = 4;    // blocks (x 32 elements) per K stage
-constexpr int kARow = kKB * 32 + 8;  // LDS bytes per activation row (padded: conflict-free b64 reads)
+constexpr int kMagicBits = 0x4B400000;  // 1.5 * 2^23
+constexpr float kMagic = 12582912.0f;
+constexpr float kHugeXs = 0x1p90f;      // activation scales from here on take the exact path
 
-// Bytes of weight codes per block in HBM, per format; in LDS every format
-// holds 32 one-byte codes per block (Q4 nibbles are expanded when a stage is
-// stored, once per workgroup instead of once per wave that reads them).
-template <int FMT>
-constexpr int wcode_bytes() {
-    return FMT == SLLM_Q8_0 ? 32 : 16;
-}
-template <int FMT>
-constexpr int brow_bytes() {
-    return kKB * 32 + 8;  // padded
-}
+__host__ __device__ constexpr int row_bytes(int KB) { return KB * 32 + 16; }  // padded: conflict-free b128 reads
 
-template <int FMT, int BN>
+template <int FMT, int KB, int BM, int BN>
 struct alignas(16) Stage {
-    // LDS image of one K stage
-    int8_t a[kBM * kARow];                       // activation codes
-    int8_t b[BN * brow_bytes<FMT>()];            // weight codes
-    float xs[kKB][kBM];                          // activation scales
-    int sx[kKB][kBM];                            // Σxq (Q4_1 / Q5K1: float(Σxq), exact, as bits)
-    // weight scales and mins, decoded to fp32 once per workgroup (Q8_0: the
-    // reference's f16 table, the others exact)
-    float d[kKB][BN];
-    float m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? kKB : 1][BN];
-    float dh[FMT == SLLM_Q5K1 ? kKB : 1][BN];
-    uint32_t hb[FMT == SLLM_Q5K1 ? kKB : 1][BN];
+    static constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    static constexpr bool DUAL = FMT == SLLM_Q5K1;
+    int8_t a[BM * row_bytes(KB)];                          // activation codes
+    int8_t b[BN * row_bytes(KB)];  // weight codes (Q4_0: nib - 8, Q4_1 / Q5K1: nib, one per byte)
+    int8_t bh[(DUAL ? BN : 1) * row_bytes(KB)];            // Q5K1 high bits as 0 / 1 bytes
+    float xs[KB][BM];                                      // activation scales
+    int aux[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? KB : 1][BM];  // float(Σxq) bits (exact, |Σxq| < 2^24)
+    float d[KB][BN];                                       // weight scales (Q8_0: the reference's f16 table)
+    float m[HAS_MIN ? KB : 1][BN];                         // mins
+    float dh[DUAL ? KB : 1][BN];                           // Q5K1 high-block scales
+    int tag;  // the K stage index whose data needs the exact epilogue (any thread that sees it writes it)
 };
 
-// Global -> register staging of one K stage (issued before the compute of the
-// previous stage, stored to LDS after it). T threads.
-template <int FMT, int BN, int T>
+// Global -> register staging of one K stage, T threads; unit e of each kind is
+// (row e / KB, block e % KB).
+template <int FMT, int KB, int BM, int BN, int T>
 struct Fetch {
-    static constexpr int A_N = kBM * kKB * 32 / 16;              // int4 of activation codes
-    static constexpr int B_N = BN * kKB * wcode_bytes<FMT>() / 16; // int4 of weight codes
-    static constexpr int S_N = kKB * kBM;                         // activation scalars
-    static constexpr int W_N = kKB * BN;                          // weight scalars
+    static constexpr int A_N = BM * KB, B_N = BN * KB;
     static constexpr int A_PER = (A_N + T - 1) / T, B_PER = (B_N + T - 1) / T;
-    static constexpr int S_PER = (S_N + T - 1) / T, W_PER = (W_N + T - 1) / T;
-    int4 a[A_PER];
-    int4 b[B_PER];
-    float xs[S_PER];
-    int sx[S_PER];
-    uint16_t d[W_PER], m[W_PER], dh[W_PER];
-    uint32_t hb[W_PER];
+    static constexpr bool Q8 = FMT == SLLM_Q8_0;
+    int4 a[A_PER][2];
+    int4 b[B_PER][Q8 ? 2 : 1];
+    float xs[A_PER];
+    int sx[A_PER];
+    uint16_t d[B_PER], m[B_PER], dh[B_PER];
+    uint32_t hb[B_PER];
 };
 
-template <int FMT, int BN, int T>
-__device__ __forceinline__ void fetch_stage(Fetch<FMT, BN, T> &f, const Planes &P, const int8_t *__restrict__ xq,
-                                            const float *__restrict__ xs, const int *__restrict__ sx, int m0,
-                                            int n0, int M, int N, int G, int g0) {
-    using F = Fetch<FMT, BN, T>;
+template <int FMT, int KB, int BM, int BN, int T>
+__device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const Planes &P,
+                                            const int8_t *__restrict__ xq, const float *__restrict__ xs,
+                                            const int *__restrict__ sx, int m0, int n0, int M, int N, int G,
+                                            int g0) {
+    using F = Fetch<FMT, KB, BM, BN, T>;
     const int tid = threadIdx.x;
-    const int K = G * 32;
-    constexpr int A_ROW_INT4 = kKB * 2;
+    const size_t K = (size_t)G * 32;
 #pragma unroll
     for (int i = 0; i < F::A_PER; i++) {
         const int e = tid + T * i;
         if (F::A_N % T == 0 || e < F::A_N) {
-            const int r = e / A_ROW_INT4, c = e % A_ROW_INT4;
-            const int m = min(m0 + r, M - 1);
-            f.a[i] = *(const int4 *)(xq + (size_t)m * K + (size_t)g0 * 32 + c * 16);
+            const int m = min(m0 + e / KB, M - 1);  // rows past M reload the last row; never stored
+            const int4 *p = (const int4 *)(xq + (size_t)m * K + (size_t)(g0 + e % KB) * 32);
+            f.a[i][0] = p[0];
+            f.a[i][1] = p[1];
+            const size_t si = (size_t)m * G + g0 + e % KB;
+            f.xs[i] = xs[si];
+            f.sx[i] = sx[si];
         }
     }
-    constexpr int WB = wcode_bytes<FMT>() / 16;  // int4 per block (2 for Q8_0: qs, qs2)
 #pragma unroll
     for (int i = 0; i < F::B_PER; i++) {
         const int e = tid + T * i;
         if (F::B_N % T == 0 || e < F::B_N) {
-            const int r = e / (kKB * WB), rem = e % (kKB * WB);
-            const int blk = rem / WB, half = rem % WB;
-            const int n = min(n0 + r, N - 1);
-            const size_t idx = (size_t)n * G + g0 + blk;
-            f.b[i] = (FMT == SLLM_Q8_0 && half) ? P.qs2[idx] : P.qs[idx];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < F::S_PER; i++) {
-        const int e = tid + T * i;
-        if (F::S_N % T == 0 || e < F::S_N) {
-            const int blk = e / kBM, r = e % kBM;
-            const int m = min(m0 + r, M - 1);
-            f.xs[i] = xs[(size_t)m * G + g0 + blk];
-            f.sx[i] = sx[(size_t)m * G + g0 + blk];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < F::W_PER; i++) {
-        const int e = tid + T * i;
-        if (F::W_N % T == 0 || e < F::W_N) {
-            const int blk = e / BN, c = e % BN;
-            const int n = min(n0 + c, N - 1);
-            const size_t idx = (size_t)n * G + g0 + blk;
+            const int n = min(n0 + e / KB, N - 1);
+            const size_t idx = (size_t)n * G + g0 + e % KB;
+            f.b[i][0] = P.qs[idx];
+            if (F::Q8) f.b[i][F::Q8 ? 1 : 0] = P.qs2[idx];
             f.d[i] = P.d[idx];
             if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) f.m[i] = P.m[idx];
             if (FMT == SLLM_Q5K1) {
@@ -138,94 +128,265 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, BN, T> &f, const Planes &
     }
 }
 
-template <int FMT, int BN, int T>
-__device__ __forceinline__ void store_stage(const Fetch<FMT, BN, T> &f, Stage<FMT, BN> &S) {
-    using F = Fetch<FMT, BN, T>;
+__device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7c00u) == 0x7c00u; }
+
+// 8 bits -> 8 bytes of 0 / 1 (bit i -> byte i).
+__device__ __forceinline__ int2 spread8(uint32_t b) {
+    return make_int2(spread4(b & 0xfu), spread4((b >> 4) & 0xfu));
+}
+
+// Stores the fetched stage `stage` into LDS in the MFMA's element order; a
+// thread that sees a scale needing the exact epilogue writes `stage` to S.tag.
+template <int FMT, int KB, int BM, int BN, int T>
+__device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, Stage<FMT, KB, BM, BN> &S,
+                                            int stage) {
+    using F = Fetch<FMT, KB, BM, BN, T>;
+    constexpr int RB = row_bytes(KB);
     const int tid = threadIdx.x;
-    constexpr int A_ROW_INT4 = kKB * 2;
+    bool slow = false;
 #pragma unroll
     for (int i = 0; i < F::A_PER; i++) {
         const int e = tid + T * i;
         if (F::A_N % T == 0 || e < F::A_N) {
-            const int r = e / A_ROW_INT4, c = e % A_ROW_INT4;
-            int2 *p = (int2 *)(S.a + r * kARow + c * 16);  // padded rows: 8-byte aligned
-            p[0] = make_int2(f.a[i].x, f.a[i].y);
-            p[1] = make_int2(f.a[i].z, f.a[i].w);
+            const int r = e / KB, blk = e % KB;
+            // elements 0..15 = (x, y | z, w), 16..31 = (x, y | z, w) of the second int4
+            const int4 lo = f.a[i][0], hi = f.a[i][1];
+            int4 *p = (int4 *)(S.a + r * RB + blk * 32);
+            p[0] = make_int4(lo.x, lo.y, hi.x, hi.y);
+            p[1] = make_int4(lo.z, lo.w, hi.z, hi.w);
+            S.xs[blk][r] = f.xs[i];
+            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) S.aux[blk][r] = __float_as_int((float)f.sx[i]);
+            slow |= !(f.xs[i] < kHugeXs);
         }
     }
-    constexpr int WB = wcode_bytes<FMT>() / 16;
 #pragma unroll
     for (int i = 0; i < F::B_PER; i++) {
         const int e = tid + T * i;
         if (F::B_N % T == 0 || e < F::B_N) {
-            const int r = e / (kKB * WB), rem = e % (kKB * WB);
-            const int blk = rem / WB, half = rem % WB;
-            int2 *p = (int2 *)(S.b + r * brow_bytes<FMT>() + blk * 32 + half * 16);
-            if (FMT == SLLM_Q8_0) {
-                p[0] = make_int2(f.b[i].x, f.b[i].y);
-                p[1] = make_int2(f.b[i].z, f.b[i].w);
+            const int r = e / KB, blk = e % KB;
+            int4 *p = (int4 *)(S.b + r * RB + blk * 32);
+            if (F::Q8) {
+                const int4 lo = f.b[i][0], hi = f.b[i][F::Q8 ? 1 : 0];
+                p[0] = make_int4(lo.x, lo.y, hi.x, hi.y);
+                p[1] = make_int4(lo.z, lo.w, hi.z, hi.w);
             } else {
-                // byte j holds element j (low nibble) and j + 16 (high nibble)
-                const int lo = 0x0f0f0f0f;
-                p[0] = make_int2(f.b[i].x & lo, f.b[i].y & lo);
-                p[1] = make_int2(f.b[i].z & lo, f.b[i].w & lo);
-                p[2] = make_int2((f.b[i].x >> 4) & lo, (f.b[i].y >> 4) & lo);
-                p[3] = make_int2((f.b[i].z >> 4) & lo, (f.b[i].w >> 4) & lo);
+                // byte j holds element j (low nibble) and element j + 16 (high nibble)
+                const int4 v = f.b[i][0];
+                int c[8] = {v.x & 0x0f0f0f0f, v.y & 0x0f0f0f0f, (v.x >> 4) & 0x0f0f0f0f, (v.y >> 4) & 0x0f0f0f0f,
+                            v.z & 0x0f0f0f0f, v.w & 0x0f0f0f0f, (v.z >> 4) & 0x0f0f0f0f, (v.w >> 4) & 0x0f0f0f0f};
+                if (FMT == SLLM_Q4_0) {
+                    // the signed code nib - 8 per byte (q4q8.go:37-43): 0x80 + nib - 8 never
+                    // borrows across bytes, and ^ 0x80 gives (nib - 8) mod 256
+#pragma unroll
+                    for (int k = 0; k < 8; k++) c[k] = ((c[k] | (int)0x80808080) - 0x08080808) ^ (int)0x80808080;
+                }
+                p[0] = make_int4(c[0], c[1], c[2], c[3]);
+                p[1] = make_int4(c[4], c[5], c[6], c[7]);
             }
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < F::S_PER; i++) {
-        const int e = tid + T * i;
-        if (F::S_N % T == 0 || e < F::S_N) {
-            const int blk = e / kBM, r = e % kBM;
-            S.xs[blk][r] = f.xs[i];
-            // the float form is converted once here instead of per output
-            S.sx[blk][r] = (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? __float_as_int((float)f.sx[i]) : f.sx[i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < F::W_PER; i++) {
-        const int e = tid + T * i;
-        if (F::W_N % T == 0 || e < F::W_N) {
-            const int blk = e / BN, c = e % BN;
-            S.d[blk][c] = (FMT == SLLM_Q8_0) ? f16_lut(f.d[i]) : f16_exact(f.d[i]);
-            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1)
-                S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][c] = f16_exact(f.m[i]);
+            S.d[blk][r] = (FMT == SLLM_Q8_0) ? f16_lut(f.d[i]) : f16_exact(f.d[i]);
+            slow |= f16_nonfinite(f.d[i]);
+            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) {
+                S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][r] = f16_exact(f.m[i]);
+                slow |= f16_nonfinite(f.m[i]);
+            }
             if (FMT == SLLM_Q5K1) {
-                S.dh[FMT == SLLM_Q5K1 ? blk : 0][c] = f16_exact(f.dh[i]);
-                S.hb[FMT == SLLM_Q5K1 ? blk : 0][c] = f.hb[i];
+                S.dh[FMT == SLLM_Q5K1 ? blk : 0][r] = f16_exact(f.dh[i]);
+                slow |= f16_nonfinite(f.dh[i]);
+                const uint32_t hb = f.hb[i];  // bit e = high bit of element e
+                int4 *q = (int4 *)(S.bh + r * RB + blk * 32);
+                const int2 c0 = spread8(hb & 0xffu), c1 = spread8((hb >> 8) & 0xffu);
+                const int2 c2 = spread8((hb >> 16) & 0xffu), c3 = spread8(hb >> 24);
+                q[0] = make_int4(c0.x, c0.y, c2.x, c2.y);
+                q[1] = make_int4(c1.x, c1.y, c3.x, c3.y);
+            }
+        }
+    }
+    if (slow) S.tag = stage;
+}
+
+// The LDS operands of one 32-element block for one wave's 32 x (32 CF) tile:
+// the MFMA operands and the scales the epilogue applies.
+template <int FMT, int CF>
+struct Ops {
+    static constexpr bool DUAL = FMT == SLLM_Q5K1;
+    static constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    v4i a;
+    v4i b[CF], bh[DUAL ? CF : 1];
+    float xv[16];                   // activation scales of the lane's 16 rows
+    int av[HAS_MIN ? 16 : 1];       // float(Σxq) of those rows
+    float wd[CF], wm[HAS_MIN ? CF : 1], wdh[DUAL ? CF : 1];
+};
+
+template <int FMT, int KB, int BM, int BN, int CF>
+__device__ __forceinline__ void load_ops(Ops<FMT, CF> &o, const Stage<FMT, KB, BM, BN> &S, int blk, int wm, int wn,
+                                         int lane) {
+    constexpr int RB = row_bytes(KB);
+    using O = Ops<FMT, CF>;
+    const int r32 = lane & 31, h = lane >> 5;
+    o.a = *(const v4i *)(S.a + (wm * 32 + r32) * RB + blk * 32 + 16 * h);
+#pragma unroll
+    for (int j = 0; j < CF; j++) {
+        const int col = wn * 32 * CF + 32 * j + r32;
+        o.b[j] = *(const v4i *)(S.b + col * RB + blk * 32 + 16 * h);
+        if (O::DUAL) o.bh[O::DUAL ? j : 0] = *(const v4i *)(S.bh + col * RB + blk * 32 + 16 * h);
+        o.wd[j] = S.d[blk][col];
+        if (O::HAS_MIN) o.wm[O::HAS_MIN ? j : 0] = S.m[O::HAS_MIN ? blk : 0][col];
+        if (O::DUAL) o.wdh[O::DUAL ? j : 0] = S.dh[O::DUAL ? blk : 0][col];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const float4 t = *(const float4 *)&S.xs[blk][wm * 32 + 8 * q + 4 * h];
+        o.xv[4 * q] = t.x; o.xv[4 * q + 1] = t.y; o.xv[4 * q + 2] = t.z; o.xv[4 * q + 3] = t.w;
+        if (O::HAS_MIN) {
+            const int4 u = *(const int4 *)&S.aux[O::HAS_MIN ? blk : 0][wm * 32 + 8 * q + 4 * h];
+            o.av[O::HAS_MIN ? 4 * q : 0] = u.x;
+            o.av[O::HAS_MIN ? 4 * q + 1 : 0] = u.y;
+            o.av[O::HAS_MIN ? 4 * q + 2 : 0] = u.z;
+            o.av[O::HAS_MIN ? 4 * q + 3 : 0] = u.w;
+        }
+    }
+}
+
+// MFMA of column piece j: D = the bits of 1.5 * 2^23 + each block dot.
+template <int FMT, int CF>
+__device__ __forceinline__ void mfma_piece(const Ops<FMT, CF> &o, int j, const v16i &cmag, v16i &D, v16i &Dh) {
+    D = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b[j], cmag, 0, 0, 0);
+    if (Ops<FMT, CF>::DUAL) Dh = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.bh[Ops<FMT, CF>::DUAL ? j : 0], cmag, 0, 0, 0);
+}
+
+// Epilogue of column piece j: SLOW is the reference's exact operation order.
+template <int FMT, int CF, bool SLOW>
+__device__ __forceinline__ void epilogue_piece(const Ops<FMT, CF> &o, int j, const v16i &D, const v16i &Dh,
+                                               float (&acc)[CF][16]) {
+    using O = Ops<FMT, CF>;
+    const float wd = o.wd[j];
+    const float wmn = O::HAS_MIN ? o.wm[O::HAS_MIN ? j : 0] : 0.0f;
+    const float wdh = O::DUAL ? o.wdh[O::DUAL ? j : 0] : 0.0f;
+    if (!SLOW) {
+        const float cd = -kMagic * wd, cdh = -kMagic * wdh;  // exact: 2 significant bits x an f16
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            float t = __builtin_fmaf(__int_as_float(D[v]), wd, cd);
+            if (O::HAS_MIN) t = __builtin_fmaf(__int_as_float(o.av[O::HAS_MIN ? v : 0]), wmn, t);
+            if (O::DUAL) t = t + __builtin_fmaf(__int_as_float(Dh[v]), wdh, cdh);
+            acc[j][v] = __builtin_fmaf(t, o.xv[v], acc[j][v]);
+        }
+    } else {
+        // the reference's operation order (no contraction)
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const float dot = __int_as_float(D[v]) - kMagic;  // exact
+            if (FMT == SLLM_Q8_0 || FMT == SLLM_Q4_0) {
+                // q8q8.go:193-195 + vnni_amd64.s:70-73; q4q8.go:37-43
+                const float cmb = wd * o.xv[v];
+                const float term = cmb * dot;
+                acc[j][v] = acc[j][v] + term;
+            } else {
+                // q41q8_row_amd64.s:65-71
+                const float t1 = dot * wd;
+                const float t2 = __int_as_float(o.av[O::HAS_MIN ? v : 0]) * wmn;
+                float tt = t1 + t2;
+                tt = tt * o.xv[v];
+                acc[j][v] = acc[j][v] + tt;
+                if (O::DUAL) {
+                    // the high block's min is +0 (convertQ5KToTwoQ41): its term is float(dot) * dh * xs
+                    const float h1 = (__int_as_float(Dh[v]) - kMagic) * wdh;
+                    const float hh = h1 * o.xv[v];
+                    acc[j][v] = acc[j][v] + hh;
+                }
             }
         }
     }
 }
 
-// B operand from LDS: 8 codes (chunk c of the block) of weight row `row`.
-template <int FMT, int BN>
-__device__ __forceinline__ long b_frag(const Stage<FMT, BN> &S, int row, int blk, int c) {
-    return *(const long *)(S.b + row * brow_bytes<FMT>() + blk * 32 + c * 8);
+// Debug: every block dot of column piece j to dots[((m * N + n) * G + g) * (1 | 2) + part].
+template <int FMT, int CF>
+__device__ __forceinline__ void dots_piece(int j, const v16i &D, const v16i &Dh, int *dots, int m0, int n0, int wm,
+                                           int wn, int lane, int M, int N, int G, int g) {
+    const int r32 = lane & 31, h = lane >> 5;
+    const int n = n0 + wn * 32 * CF + 32 * j + r32;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (m < M && n < N) {
+            const size_t o = ((size_t)m * N + n) * G + g;
+            if (FMT == SLLM_Q5K1) {
+                dots[2 * o] = D[v] - kMagicBits;
+                dots[2 * o + 1] = Dh[v] - kMagicBits;
+            } else {
+                dots[o] = D[v] - kMagicBits;
+            }
+        }
+    }
 }
 
-// Q5K1 high operand: elements 8c..8c+7 of the mask as 0/1 bytes.
-__device__ __forceinline__ long bits_frag(uint32_t hb, int c) {
-    const uint32_t t = hb >> (8 * c);
-    return (long)((uint64_t)(uint32_t)spread4(t) | ((uint64_t)(uint32_t)spread4(t >> 4) << 32));
+// The NB blocks blk0, blk0 + WK, ... of one K stage for one wave, software-
+// pipelined: block i+1's LDS operands are read before block i's epilogue, and
+// its MFMA for piece j is issued as soon as block i's epilogue has consumed
+// piece j's results, so the LDS and MFMA latencies of the next block overlap
+// the current block's VALU work.
+template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool DBG>
+__device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
+                                           const v16i &cmag, float (&acc)[CF][16], int *dots, int m0, int n0, int M,
+                                           int N, int G, int g0) {
+    Ops<FMT, CF> ops[2];
+    v16i D[CF], Dh[CF];
+    load_ops<FMT, KB, BM, BN, CF>(ops[0], S, blk0, wm, wn, lane);
+#pragma unroll
+    for (int j = 0; j < CF; j++) mfma_piece<FMT, CF>(ops[0], j, cmag, D[j], Dh[j]);
+#pragma unroll
+    for (int i = 0; i < NB; i++) {
+        Ops<FMT, CF> &cur = ops[i & 1];
+        Ops<FMT, CF> &nxt = ops[(i + 1) & 1];
+        if (i + 1 < NB) load_ops<FMT, KB, BM, BN, CF>(nxt, S, blk0 + (i + 1) * WK, wm, wn, lane);
+        // keep the next block's LDS reads ahead of this block's epilogue
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < CF; j++) {
+            if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
+            epilogue_piece<FMT, CF, false>(cur, j, D[j], Dh[j], acc);
+            if (i + 1 < NB) mfma_piece<FMT, CF>(nxt, j, cmag, D[j], Dh[j]);
+        }
+    }
 }
 
-// Workgroup = 2 x WN waves; tile 64 x BN (BN = 32 WN); K stages [st0, st1).
-template <int FMT, int WN>
-__global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *__restrict__ xq,
-                                                        const float *__restrict__ xs, const int *__restrict__ sx,
-                                                        float *__restrict__ out, int M, int N, int G, int mtiles,
-                                                        int ntiles, int splits, int sps) {
-    constexpr int BN = 32 * WN, T = 128 * WN;
-    constexpr bool DUAL = FMT == SLLM_Q5K1;
+// The same blocks in the reference's exact operation order, one at a time.
+template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool DBG>
+__device__ __forceinline__ void stage_slow(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
+                                           const v16i &cmag, float (&acc)[CF][16], int *dots, int m0, int n0, int M,
+                                           int N, int G, int g0) {
+#pragma unroll 1
+    for (int i = 0; i < NB; i++) {
+        Ops<FMT, CF> o;
+        load_ops<FMT, KB, BM, BN, CF>(o, S, blk0 + i * WK, wm, wn, lane);
+#pragma unroll
+        for (int j = 0; j < CF; j++) {
+            v16i D, Dh;
+            mfma_piece<FMT, CF>(o, j, cmag, D, Dh);
+            if (DBG) dots_piece<FMT, CF>(j, D, Dh, dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
+            epilogue_piece<FMT, CF, true>(o, j, D, Dh, acc);
+        }
+    }
+}
+
+// Workgroup = WM x WN x WK waves; tile (32 WM) x (32 CF WN); K stages [st0, st1).
+// DBG: also write every block dot to dots[((m * N + n) * G + g) * (1 | 2) + part].
+template <int FMT, int WM, int WN, int CF, int WK, int KB, bool DBG>
+__global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(
+    Planes P, const int8_t *__restrict__ xq, const float *__restrict__ xs, const int *__restrict__ sx,
+    float *__restrict__ out, int M, int N, int G, int mtiles, int ntiles, int splits, int sps,
+    int *__restrict__ dots) {
+    constexpr int BM = 32 * WM, BN = 32 * CF * WN, T = 64 * WM * WN * WK;
+    static_assert(KB % WK == 0, "every wave takes the same number of blocks per stage");
+    static_assert(CF % 2 == 0, "column pieces go in pairs");
+    using St = Stage<FMT, KB, BM, BN>;
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-    Stage<FMT, BN> *stages = (Stage<FMT, BN> *)lds_raw;
+    St *stages = (St *)lds_raw;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int wk = wave / (WM * WN), wmn = wave % (WM * WN);
+    const int wm = wmn % WM, wn = wmn / WM;
     // XCD-aware order: workgroup id -> XCD (id % 8); consecutive linear indices
     // (the M-tiles of one weight tile and split) stay on one XCD, so that
     // weight tile comes from HBM once into that XCD's L2.
@@ -236,119 +397,75 @@ __global__ void __launch_bounds__(128 * WN) gemm_kernel(Planes P, const int8_t *
     const int mt = lin % mtiles;
     const int rest = lin / mtiles;
     const int sp = rest % splits, nt = rest / splits;
-    const int m0 = mt * kBM, n0 = nt * BN;
-    const int r16 = lane & 15, c4 = lane >> 4;
-    const int nst = G / kKB;
+    const int m0 = mt * BM, n0 = nt * BN;
+    const int nst = G / KB;
     const int st0 = sp * sps, st1 = min(nst, st0 + sps);
 
-    float acc[2][2][4], acc2[DUAL ? 2 : 1][DUAL ? 2 : 1][4];
+    float acc[CF][16];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int j = 0; j < CF; j++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
+    v16i cmag;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                acc[i][j][r] = 0.0f;
-                acc2[DUAL ? i : 0][DUAL ? j : 0][r] = 0.0f;
-            }
+    for (int v = 0; v < 16; v++) cmag[v] = kMagicBits;
 
-    Fetch<FMT, BN, T> f;
+    if (threadIdx.x == 0) stages[0].tag = stages[1].tag = -1;
+    __syncthreads();
+    Fetch<FMT, KB, BM, BN, T> f;
     if (st0 < st1) {
-        fetch_stage<FMT, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * kKB);
-        store_stage<FMT, BN, T>(f, stages[0]);
+        fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
+        store_stage<FMT, KB, BM, BN, T>(f, stages[0], st0);
     }
     __syncthreads();
 
     for (int s = st0; s < st1; s++) {
-        if (s + 1 < st1) fetch_stage<FMT, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * kKB);
-        const Stage<FMT, BN> &S = stages[(s - st0) & 1];
-#pragma unroll 1
-        for (int blk = 0; blk < kKB; blk++) {
-            long a[2];
-            float4 xsr[2];
-            int4 sxr[2];
-#pragma unroll
-            for (int i = 0; i < 2; i++) {
-                const int row = wm * 32 + 16 * i;
-                a[i] = *(const long *)(S.a + (row + r16) * kARow + blk * 32 + c4 * 8);
-                xsr[i] = *(const float4 *)&S.xs[blk][row + 4 * c4];
-                sxr[i] = *(const int4 *)&S.sx[blk][row + 4 * c4];
-            }
-#pragma unroll
-            for (int j = 0; j < 2; j++) {
-                const int col = wn * 32 + 16 * j + r16;
-                const long b = b_frag<FMT, BN>(S, col, blk, c4);
-                const float wd = S.d[blk][col];
-                float wmn = 0.0f, wdh = 0.0f;
-                long bh = 0;
-                if (FMT == SLLM_Q4_1 || DUAL) wmn = S.m[(FMT == SLLM_Q4_1 || DUAL) ? blk : 0][col];
-                if (DUAL) {
-                    wdh = S.dh[DUAL ? blk : 0][col];
-                    bh = bits_frag(S.hb[DUAL ? blk : 0][col], c4);
-                }
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const v4i z = {0, 0, 0, 0};
-                    const v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], b, z, 0, 0, 0);
-                    const float xv[4] = {xsr[i].x, xsr[i].y, xsr[i].z, xsr[i].w};
-                    const int sv[4] = {sxr[i].x, sxr[i].y, sxr[i].z, sxr[i].w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        if (FMT == SLLM_Q8_0) {
-                            // q8q8.go:193-195 + vnni_amd64.s:70-73
-                            const float cmb = wd * xv[r];
-                            const float term = cmb * (float)d[r];
-                            acc[i][j][r] = acc[i][j][r] + term;
-                        } else if (FMT == SLLM_Q4_0) {
-                            // q4q8.go:37-43
-                            const float cmb = wd * xv[r];
-                            const float term = cmb * (float)(d[r] - 8 * sv[r]);
-                            acc[i][j][r] = acc[i][j][r] + term;
-                        } else {
-                            // q41q8_row_amd64.s:65-71
-                            const float t1 = (float)d[r] * wd;
-                            const float t2 = __int_as_float(sv[r]) * wmn;
-                            float tt = t1 + t2;
-                            tt = tt * xv[r];
-                            acc[i][j][r] = acc[i][j][r] + tt;
-                        }
-                    }
-                    if (DUAL) {
-                        const v4i h = __builtin_amdgcn_mfma_i32_16x16x32_i8(a[i], bh, z, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 4; r++) {
-                            // The reference's high pass adds float(Σxq) * (+0), a
-                            // signed zero (Σxq is finite): h1 + ±0 is h1 unless h1
-                            // is itself a zero, and a zero term leaves acc2 (which
-                            // starts at +0, so is never -0) unchanged whatever its
-                            // sign. Omitting that add gives the same acc2 bits.
-                            const float h1 = (float)h[r] * wdh;
-                            const float hh = h1 * xv[r];
-                            acc2[DUAL ? i : 0][DUAL ? j : 0][r] = acc2[DUAL ? i : 0][DUAL ? j : 0][r] + hh;
-                        }
-                    }
-                }
-            }
-        }
-        if (s + 1 < st1) store_stage<FMT, BN, T>(f, stages[(s + 1 - st0) & 1]);
+        if (s + 1 < st1) fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * KB);
+        const St &S = stages[(s - st0) & 1];
+        if (S.tag != s)
+            stage_fast<FMT, KB, BM, BN, CF, KB / WK, WK, DBG>(S, wk, wm, wn, lane, cmag, acc, dots, m0, n0, M, N, G,
+                                                              s * KB);
+        else
+            stage_slow<FMT, KB, BM, BN, CF, KB / WK, WK, DBG>(S, wk, wm, wn, lane, cmag, acc, dots, m0, n0, M, N, G,
+                                                              s * KB);
+        if (s + 1 < st1) store_stage<FMT, KB, BM, BN, T>(f, stages[(s + 1 - st0) & 1], s + 1);
         __syncthreads();
     }
 
+    // add the WK partial tiles: wk + step into wk, step = WK/2 .. 1 (fixed tree order)
+    if (WK > 1) {
+        float *red = (float *)lds_raw;  // [WK/2][WM*WN][16 * CF][64]
+#pragma unroll
+        for (int step = WK / 2; step >= 1; step /= 2) {
+            if (wk >= step && wk < 2 * step) {
+                float *r = red + ((size_t)((wk - step) * WM * WN + wmn) * 16 * CF) * 64;
+#pragma unroll
+                for (int j = 0; j < CF; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) r[(j * 16 + v) * 64 + lane] = acc[j][v];
+            }
+            __syncthreads();
+            if (wk < step) {
+                const float *r = red + ((size_t)(wk * WM * WN + wmn) * 16 * CF) * 64;
+#pragma unroll
+                for (int j = 0; j < CF; j++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++) acc[j][v] = acc[j][v] + r[(j * 16 + v) * 64 + lane];
+            }
+            __syncthreads();
+        }
+        if (wk != 0) return;
+    }
+
+    const int r32 = lane & 31, h = lane >> 5;
     float *o = out + (size_t)sp * M * N;  // splits > 1: partial tile of split sp
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int j = 0; j < CF; j++) {
+        const int n = n0 + wn * 32 * CF + 32 * j + r32;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + wn * 32 + 16 * j + r16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + wm * 32 + 16 * i + 4 * c4 + r;
-                if (m < M && n < N) {
-                    float v = acc[i][j][r];
-                    if (DUAL) v = v + acc2[DUAL ? i : 0][DUAL ? j : 0][r];
-                    o[(size_t)m * N + n] = v;
-                }
-            }
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m < M && n < N) o[(size_t)m * N + n] = acc[j][v];
         }
     }
 }
@@ -523,14 +640,19 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
     }
 }
 
+// Workgroup shapes of the int8 GEMM: (waves along M, along N, along K, blocks per stage).
+// kWide: 64 x 128 tiles, 4 waves of 32 x 64; kDeep: 64 x 64 tiles, 4 waves of
+// 32 x 64, two of which take alternate blocks of each K stage. 4-block stages.
+enum GemmShape { kWide = 0, kDeep = 1 };
+
 struct GemmPlan {
-    int wn, splits, sps, mtiles, ntiles;
+    int shape, bn, kb, splits, sps, mtiles, ntiles;
 };
 
 GemmPlan plan_gemm_q5(int M, int N, int G) {
     const int cus = 256;
     GemmPlan p{};
-    p.wn = 0;
+    p.shape = 0;
     p.mtiles = (M + kQ5Tile - 1) / kQ5Tile;
     p.ntiles = (N + kQ5Tile - 1) / kQ5Tile;
     int S = 1;
@@ -540,76 +662,82 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
     return p;
 }
 
+constexpr int kGemmBM = 64;
+constexpr int shape_bn(int fmt, int shape) { return shape == kDeep ? 64 : 128; }
+constexpr int shape_kb(int shape) { return 4; }
+
 GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     if (fmt == SLLM_Q5_0) return plan_gemm_q5(M, N, G);
     const int cus = 256;
     GemmPlan p{};
-    p.mtiles = (M + kBM - 1) / kBM;
-    auto tiles = [&](int wn) { return (int64_t)p.mtiles * ((N + 32 * wn - 1) / (32 * wn)); };
-    // 8-wave workgroups (64 x 128 tiles) from 64 such tiles, else 4-wave ones;
-    // then K splits double until there are 1.5 workgroups per CU, each split
-    // keeping >= 4 stages. Measured at M = 64 / 128 (µs): Q4_1 14336x4096
-    // 44-46 -> 39-40 / 70-74 -> 62 against 4-wave tiles with 2 workgroups per
-    // CU; Q8_0 4096x14336 at M = 64 keeps 4-wave tiles (35-38; 8-wave ones
-    // 40); 2-wave workgroups were slower everywhere (Q8_0 at M = 64: 50)
-    p.wn = tiles(4) >= 64 ? 4 : 2;
-    if (tuning().gemm_wn) p.wn = tuning().gemm_wn;
-    p.ntiles = (N + 32 * p.wn - 1) / (32 * p.wn);
-    const int nst = G / kKB;
+    // Q5K1 (two MFMAs and a longer epilogue per block, so twice the registers
+    // per output) on the narrow tiles whose waves split each K stage; the other
+    // formats on the wide ones. Measured on C3 / C4 shapes at M = 64, 128, 512:
+    // wide Q4_1 14336x4096 36 / 57 / 173 us against 41 / 62 / 212 narrow, Q8_0
+    // 4096x14336 37 / 54 / 150 against 37 / 59 / 180; Q5K1 14336x4096 narrow
+    // 59 / 95 / 311 against 100 / 167 / 577 wide (its wide tiles spill).
+    p.shape = fmt == SLLM_Q5K1 ? kDeep : kWide;
+    if (tuning().gemm_shape == 1) p.shape = kWide;
+    if (tuning().gemm_shape == 2 && G % shape_kb(kDeep) == 0) p.shape = kDeep;
+    p.bn = shape_bn(fmt, p.shape);
+    p.kb = shape_kb(p.shape);
+    p.mtiles = (M + kGemmBM - 1) / kGemmBM;
+    p.ntiles = (N + p.bn - 1) / p.bn;
+    const int nst = G / p.kb;
+    // K splits double until there are 1.5 workgroups per CU, each split keeping >= 2 stages
     int S = 1;
-    while ((int64_t)p.mtiles * p.ntiles * S * 2 < 3 * cus && nst / (S * 2) >= 4) S *= 2;
+    while ((int64_t)p.mtiles * p.ntiles * S * 2 < 3 * cus && nst / (S * 2) >= 2) S *= 2;
     if (tuning().gemm_splits) S = tuning().gemm_splits < nst ? tuning().gemm_splits : nst;
     p.splits = S;
     p.sps = (nst + S - 1) / S;
     return p;
 }
 
-template <int FMT, int WN>
-sllm_status launch_wn(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
-                      int N, int G, const GemmPlan &p, hipStream_t s) {
+template <int FMT, int WM, int WN, int CF, int WK, int KB, bool DBG>
+sllm_status launch_shape(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
+                         int N, int G, const GemmPlan &p, int *dots, hipStream_t s) {
     const int total = p.mtiles * p.ntiles * p.splits;
     const int grid = ((total + 7) / 8) * 8;
-    const size_t lds = 2 * sizeof(Stage<FMT, 32 * WN>);
-    hipLaunchKernelGGL((gemm_kernel<FMT, WN>), dim3(grid), dim3(128 * WN), lds, s, P, xq, xsp, sxp, out, M, N, G,
-                       p.mtiles, p.ntiles, p.splits, p.sps);
+    constexpr size_t stages = 2 * sizeof(Stage<FMT, KB, 32 * WM, 32 * CF * WN>);
+    constexpr size_t red = (size_t)(WK / 2) * WM * WN * 16 * CF * 64 * sizeof(float);
+    constexpr size_t lds = stages > red ? stages : red;
+    static_assert(lds <= 160 * 1024, "LDS");
+    hipLaunchKernelGGL((gemm_kernel<FMT, WM, WN, CF, WK, KB, DBG>), dim3(grid), dim3(64 * WM * WN * WK), lds, s, P, xq,
+                       xsp, sxp, out, M, N, G, p.mtiles, p.ntiles, p.splits, p.sps, dots);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }
 
-template <int FMT>
+template <int FMT, bool DBG>
 sllm_status launch_fmt(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
-                       int N, int G, const GemmPlan &p, hipStream_t s) {
-    switch (p.wn) {
-    case 4: return launch_wn<FMT, 4>(P, xq, xsp, sxp, out, M, N, G, p, s);
-    case 2: return launch_wn<FMT, 2>(P, xq, xsp, sxp, out, M, N, G, p, s);
-    default: return launch_wn<FMT, 1>(P, xq, xsp, sxp, out, M, N, G, p, s);
+                       int N, int G, const GemmPlan &p, int *dots, hipStream_t s) {
+    if (p.shape == kDeep) return launch_shape<FMT, 2, 1, 2, 2, 4, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    return launch_shape<FMT, 2, 2, 2, 1, 4, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+}
+
+template <bool DBG>
+sllm_status launch_int8(int fmt, const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out,
+                        int M, int N, int G, const GemmPlan &p, int *dots, hipStream_t s) {
+    switch (fmt) {
+    case SLLM_Q8_0: return launch_fmt<SLLM_Q8_0, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case SLLM_Q4_0: return launch_fmt<SLLM_Q4_0, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case SLLM_Q4_1: return launch_fmt<SLLM_Q4_1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case SLLM_Q5K1: return launch_fmt<SLLM_Q5K1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     }
+    return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-}  // namespace
-
-bool gemm_supported(int fmt, int G) {
-    if (kq_native(fmt)) return false;  // the GEMV takes every row count
-    return fmt == SLLM_Q5_0 ? G >= 1 : G % kKB == 0;
-}
-
-size_t gemm_workspace_bytes(int fmt, int N, int G, int M) {
-    const GemmPlan p = plan_gemm(fmt, M, N, G);
-    const size_t parts = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
-    if (fmt == SLLM_Q5_0) return align256(parts);
-    return align256((size_t)M * G * 32) + 2 * align256((size_t)M * G * 4) + align256(parts);
-}
-
-sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M, void *ws,
-                        size_t ws_bytes, hipStream_t s) {
+sllm_status gemm_impl(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M, void *ws,
+                      size_t ws_bytes, int *dots, hipStream_t s) {
     if (ws_bytes < gemm_workspace_bytes(fmt, N, G, M)) return set_error(SLLM_ERR_ARG, "gemm: workspace too small");
     if (!gemm_supported(fmt, G)) return set_error(SLLM_ERR_SHAPE, "gemm: format or cols not supported");
     const GemmPlan p = plan_gemm(fmt, M, N, G);
     sllm_status st = SLLM_OK;
     float *part;
     if (fmt == SLLM_Q5_0) {
+        if (dots) return set_error(SLLM_ERR_QTYPE, "gemm block dots: Q5_0 has no int8 GEMM");
         part = (float *)ws;
         const int total = p.mtiles * p.ntiles * p.splits;
         hipLaunchKernelGGL(gemm_q5_kernel, dim3(((total + 7) / 8) * 8), dim3(256), 2 * sizeof(Q5Stage), s, P, x,
@@ -624,13 +752,8 @@ sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, in
         st = launch_quantize_act(x, M, G, xq, xsp, sxp, s);
         if (st != SLLM_OK) return st;
         float *out = p.splits > 1 ? part : dst;
-        switch (fmt) {
-        case SLLM_Q8_0: st = launch_fmt<SLLM_Q8_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-        case SLLM_Q4_0: st = launch_fmt<SLLM_Q4_0>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-        case SLLM_Q4_1: st = launch_fmt<SLLM_Q4_1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-        case SLLM_Q5K1: st = launch_fmt<SLLM_Q5K1>(P, xq, xsp, sxp, out, M, N, G, p, s); break;
-        default: return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
-        }
+        st = dots ? launch_int8<true>(fmt, P, xq, xsp, sxp, out, M, N, G, p, dots, s)
+                  : launch_int8<false>(fmt, P, xq, xsp, sxp, out, M, N, G, p, nullptr, s);
     }
     if (st != SLLM_OK || p.splits == 1) return st;
     const size_t n = (size_t)M * N;
@@ -639,6 +762,31 @@ sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, in
     hipLaunchKernelGGL(reduce_splits_kernel, dim3(grid), dim3(256), 0, s, part, dst, n, p.splits);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
+}
+
+}  // namespace
+
+bool gemm_supported(int fmt, int G) {
+    if (kq_native(fmt)) return false;  // the GEMV takes every row count
+    return fmt == SLLM_Q5_0 ? G >= 1 : G % shape_kb(kWide) == 0;
+}
+
+size_t gemm_workspace_bytes(int fmt, int N, int G, int M) {
+    const GemmPlan p = plan_gemm(fmt, M, N, G);
+    const size_t parts = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+    if (fmt == SLLM_Q5_0) return align256(parts);
+    return align256((size_t)M * G * 32) + 2 * align256((size_t)M * G * 4) + align256(parts);
+}
+
+sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M, void *ws,
+                        size_t ws_bytes, hipStream_t s) {
+    return gemm_impl(fmt, P, x, dst, N, G, M, ws, ws_bytes, nullptr, s);
+}
+
+sllm_status launch_gemm_dots(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M, void *ws,
+                             size_t ws_bytes, int32_t *dots, hipStream_t s) {
+    if (!dots) return set_error(SLLM_ERR_ARG, "gemm block dots: null output");
+    return gemm_impl(fmt, P, x, dst, N, G, M, ws, ws_bytes, dots, s);
 }
 
 }  // namespace sllm

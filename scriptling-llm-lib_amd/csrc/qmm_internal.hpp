@@ -202,6 +202,10 @@ sllm_status launch_rmsnorm(const float *x, const float *norm_w, float eps, int r
 sllm_status launch_swiglu(const float *gate, const float *up, float *h, size_t n, hipStream_t s);
 sllm_status launch_gemm(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
                         void *ws, size_t ws_bytes, hipStream_t s);
+// The same GEMM that also writes every int32 block dot its matrix cores
+// produce to dots [M][N][G] (x2 for Q5K1: low, high); int8 formats only.
+sllm_status launch_gemm_dots(int fmt, const Planes &P, const float *x, float *dst, int N, int G, int M,
+                             void *ws, size_t ws_bytes, int32_t *dots, hipStream_t s);
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M);
 bool gemm_supported(int fmt, int G);  // Q5_0 and K not a multiple of 128 stay on the GEMV
 sllm_status launch_quantize_act(const float *x, int rows, int G, int8_t *xq, float *xs, int32_t *sx,
@@ -255,7 +259,8 @@ struct Tuning {
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
-    int gemm_wn = 0;           // GEMM waves along N per workgroup / 2 (1, 2, 4; 0: by tile count)
+    int gemm_shape = 0;        // GEMM workgroup shape: 1 wide (64 x 128 tiles), 2 deep (64 x 64, K split
+                               // over two waves); 0: by row count
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
     int gemv_q6k_stream = 0;   // Q6_K weights: load (and stream) the native 6-bit planes (1) or the Q8_0 planes only (0)

@@ -101,6 +101,7 @@ def lib() -> C.CDLL:
     L.sllm_argmax_dev.argtypes = [P, i32, C.POINTER(i32), P]
     L.sllm_debug_quantize_act.argtypes = [P, i32, i32, P, P, P]
     L.sllm_debug_block_dots.argtypes = [W, P, i32, i32, P]
+    L.sllm_debug_gemm_block_dots.argtypes = [W, P, i32, i32, i32, i32, P]
     L.sllm_set_param.argtypes = [C.c_char_p, i32]
     L.sllm_matmul_add_dev.argtypes = [W, P, i32, i32, P, P]
     L.sllm_weight_stream_bytes.argtypes = [W, C.POINTER(sz)]
@@ -465,4 +466,16 @@ def debug_block_dots(w: DeviceWeight, x: np.ndarray) -> np.ndarray:
     shape = (M, w.rows, w.groups, 2) if w.qtype == "q5k1" else (M, w.rows, w.groups)
     out = np.empty(shape, np.int32)
     _check(lib().sllm_debug_block_dots(w.handle, _ptr(x), M, w.cols, _ptr(out)))
+    return out
+
+
+def debug_gemm_block_dots(w: DeviceWeight, x: np.ndarray, row0: int = 0, n_rows: int | None = None) -> np.ndarray:
+    """The int32 block dots the prefill GEMM's matrix cores produce for weight
+    rows [row0, row0 + n_rows): [M][n_rows][groups] (x2 for Q5K1)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, w.cols)
+    M = x.shape[0]
+    n = w.rows - row0 if n_rows is None else n_rows
+    shape = (M, n, w.groups, 2) if w.qtype == "q5k1" else (M, n, w.groups)
+    out = np.empty(shape, np.int32)
+    _check(lib().sllm_debug_gemm_block_dots(w.handle, _ptr(x), M, w.cols, int(row0), int(n), _ptr(out)))
     return out

@@ -63,12 +63,22 @@ def assert_fp32_parity(got: np.ndarray, ref: np.ndarray, bound: np.ndarray, what
     got = np.asarray(got, np.float64).reshape(ref.shape)
     ref = np.asarray(ref, np.float64)
     bound = np.asarray(bound, np.float64).reshape(ref.shape)
+    # special values must match exactly: NaN where the reference has NaN, the
+    # same infinity where it has one (the bound below cannot see either)
+    nan_r, nan_g = np.isnan(ref), np.isnan(got)
+    assert np.array_equal(nan_r, nan_g), f"{what}: NaN positions differ ({int(nan_r.sum())} ref, {int(nan_g.sum())} got)"
+    inf_r = np.isinf(ref)
+    assert np.array_equal(got[inf_r], ref[inf_r]) and not np.isinf(got[~inf_r]).any(), f"{what}: infinities differ"
+    fin = ~(nan_r | inf_r)
+    got, ref, bound = got[fin], ref[fin], bound[fin]
+    if got.size == 0:
+        return
     err = np.abs(got - ref)
     lim = REL_TOL * bound + 1e-30
-    bad = np.argwhere(err > lim)
+    bad = np.flatnonzero(err > lim)
     assert bad.size == 0, (
-        f"{what}: {len(bad)} outputs exceed {REL_TOL:g}*sum|terms|; first {bad[0].tolist()}: "
-        f"got {got[tuple(bad[0])]!r} ref {ref[tuple(bad[0])]!r} bound {lim[tuple(bad[0])]!r}")
+        f"{what}: {len(bad)} outputs exceed {REL_TOL:g}*sum|terms|; first (finite index {int(bad[0])}): "
+        f"got {got[bad[0]]!r} ref {ref[bad[0]]!r} bound {lim[bad[0]]!r}")
     scale = np.abs(ref).max()
     if scale > 0:
         assert err.max() / scale <= REL_TOL, f"{what}: vector-scale error {err.max() / scale:g}"

@@ -42,25 +42,95 @@ def test_prefill_parity(qtype, M, N, K):
     assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} M={M} {N}x{K}")
 
 
-@pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1"])
-@pytest.mark.parametrize("wn,splits", [(2, 1), (2, 3), (4, 5), (4, 8), (1, 2)])
-def test_tile_width_and_split_overrides(qtype, wn, splits):
-    # any tile width and K split count gives the oracle's result within the
-    # bound (K = 1024 is 8 stages: 5 splits of 2 stages leave the last split
-    # empty, and it adds a zero tile)
+@pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
+@pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1)])
+def test_shape_and_split_overrides(qtype, shape, splits):
+    # either workgroup shape and any K split count gives the oracle's result
+    # within the bound (K = 1024 is 8 or 16 stages: 5 splits leave the last
+    # split empty on the 4-block stages, and it adds a zero tile)
     N, K, M = 320, 1024, 130
-    raw = make_raw(qtype, N, K, seed=wn * 10 + splits)
+    raw = make_raw(qtype, N, K, seed=shape * 10 + splits)
     x = make_x(M, K, seed=splits)
     w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
-    sq.set_param("gemm_wn", wn)
+    sq.set_param("gemm_shape", shape)
     sq.set_param("gemm_splits", splits)
     try:
         got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
     finally:
-        sq.set_param("gemm_wn", 0)
+        sq.set_param("gemm_shape", 0)
         sq.set_param("gemm_splits", 0)
     ref = oracle.matmul(qtype, raw, N, x)
-    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} wn={wn} S={splits}")
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} shape={shape} S={splits}")
+
+
+def _block_dots_case(qtype, raw, N, K, x, row0, n_rows, shape=0):
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    sq.set_param("gemm_shape", shape)
+    try:
+        got = sq.debug_gemm_block_dots(w, x, row0, n_rows)
+    finally:
+        sq.set_param("gemm_shape", 0)
+    sub = slice_rows(qtype, raw, N, K // 32, np.arange(row0, row0 + n_rows))
+    ref = oracle.block_dots(qtype, sub, n_rows, K, x)
+    assert got.shape == ref.shape
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{qtype}: {len(bad)} block dots differ, first {bad[0].tolist()}: " \
+                          f"{got[tuple(bad[0])]} vs {ref[tuple(bad[0])]}"
+
+
+@pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
+@pytest.mark.parametrize("M", [64, 130])
+@pytest.mark.parametrize("shape", [1, 2])
+def test_gemm_block_dots_bitexact(qtype, M, shape):
+    # the int32 block dots the matrix cores return, read from the registers the
+    # epilogue scales, against the oracle's per-(row, block) dots
+    N, K = 200, 1024
+    raw = make_raw(qtype, N, K, seed=M + shape)
+    x = make_x(M, K, seed=3 * M)
+    x[1] = 0.0                       # all-zero blocks: xq 0
+    x[2, :64] = np.float32(1e30)     # one saturated block: +-127
+    _block_dots_case(qtype, raw, N, K, x, 0, N, shape)
+    _block_dots_case(qtype, raw, N, K, x, 37, 101, shape)  # a row range starting mid-tile
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("M", [64, 130])
+def test_gemm_block_dots_c3_gate_rows(M):
+    # C3 gate (Q4_K -> Q4_1, 14336 x 4096): the GEMM's block dots for the last
+    # 256 weight rows, as it computes them inside the full-shape launch plan
+    N, K = 14336, 4096
+    w = sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(11, N, K), N, K)
+    raw = w.export()
+    x = make_x(M, K, seed=M)
+    got = sq.debug_gemm_block_dots(w, x, N - 256, 256)
+    sub = slice_rows("q4_1", raw, N, K // 32, np.arange(N - 256, N))
+    assert np.array_equal(got, oracle.block_dots("q4_1", sub, 256, K, x))
+
+
+@pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
+def test_gemm_nonfinite_weight_scales(qtype):
+    # f16 Inf / NaN / max-finite weight scales and mins: those K stages take the
+    # reference's exact operation order, so Inf and NaN outputs match the oracle's
+    N, K, M = 96, 512, 64
+    raw = make_raw(qtype, N, K, seed=21).copy()
+    G = K // 32
+    bb = 20 if qtype == "q5k1" else oracle.BLOCK_BYTES[qtype]
+    blocks = raw.reshape(-1, bb)
+    specials = [0x7c00, 0xfc00, 0x7e00, 0x7bff, 0xfbff]
+    for i, v in enumerate(specials):
+        r, g = 3 + 17 * i, (5 * i) % G
+        blocks[r * G + g, 0:2] = [v & 0xff, v >> 8]
+        if qtype in ("q4_1", "q5k1"):
+            blocks[(r + 1) * G + g, 2:4] = [v & 0xff, v >> 8]   # min
+    if qtype == "q5k1":
+        blocks[N * G + 50 * G + 7, 0:2] = [0x00, 0x7c]          # high block scale +Inf
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, G, N, K))
+    x = make_x(M, K, seed=22)
+    x[5] = 0.0  # zero activation blocks: the reference's scale 0 turns Inf weight scales into NaN
+    got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert np.isnan(ref).any() and np.isinf(ref).any()
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} special scales")
 
 
 @pytest.mark.parametrize("qtype", ["q8", "q4_1", "q5k1", "q5"])
