@@ -409,9 +409,10 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
  *   gemm_min_rows       >= 1       activation rows from which the GEMM is used (64;
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)
- *   gemm_shape          0, 1, 2    GEMM workgroup tiles: 1 = 64 x 128, 2 = 64 x 64 with each
- *                                  K stage split over two waves (0: 2 for Q5K1, else 1;
- *                                  the shape moves the fp32 summation splits)
+ *   gemm_shape          0..3       GEMM workgroups: 1 = 64 x 128 tiles, 2 = 64 x 64 tiles with
+ *                                  each K stage split over two waves, 3 = as 2 with two
+ *                                  stages of loads in flight (0: 3 for Q5K1, else 1; the
+ *                                  shape moves the fp32 summation splits)
  *   gemm_splits         0..64      GEMM K splits, added in split order (0: by tile count;
  *                                  the split count moves the fp32 summation splits)
  *   attn_target_blocks  1..65536   attention: about this many workgroups when splitting (512)

@@ -325,10 +325,27 @@ __device__ __forceinline__ void dots_piece(int j, const v16i &D, const v16i &Dh,
 // its MFMA for piece j is issued as soon as block i's epilogue has consumed
 // piece j's results, so the LDS and MFMA latencies of the next block overlap
 // the current block's VALU work.
-template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool DBG>
+template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool PIPE, bool DBG>
 __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
                                            const v16i &cmag, float (&acc)[CF][16], int *dots, int m0, int n0, int M,
                                            int N, int G, int g0) {
+    if (!PIPE) {
+        // one block at a time (fewer registers: leaves room for a deeper global prefetch)
+#pragma unroll 1
+        for (int i = 0; i < NB; i++) {
+            Ops<FMT, CF> o;
+            load_ops<FMT, KB, BM, BN, CF>(o, S, blk0 + i * WK, wm, wn, lane);
+            v16i D[CF], Dh[CF];
+#pragma unroll
+            for (int j = 0; j < CF; j++) mfma_piece<FMT, CF>(o, j, cmag, D[j], Dh[j]);
+#pragma unroll
+            for (int j = 0; j < CF; j++) {
+                if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
+                epilogue_piece<FMT, CF, false>(o, j, D[j], Dh[j], acc);
+            }
+        }
+        return;
+    }
     Ops<FMT, CF> ops[2];
     v16i D[CF], Dh[CF];
     load_ops<FMT, KB, BM, BN, CF>(ops[0], S, blk0, wm, wn, lane);
@@ -371,7 +388,9 @@ __device__ __forceinline__ void stage_slow(const Stage<FMT, KB, BM, BN> &S, int 
 
 // Workgroup = WM x WN x WK waves; tile (32 WM) x (32 CF WN); K stages [st0, st1).
 // DBG: also write every block dot to dots[((m * N + n) * G + g) * (1 | 2) + part].
-template <int FMT, int WM, int WN, int CF, int WK, int KB, bool DBG>
+// PIPE: software-pipelined blocks (stage_fast); PF: K stages of global loads
+// in flight (1: the next stage while this one is computed; 2: the next two).
+template <int FMT, int WM, int WN, int CF, int WK, int KB, bool PIPE, int PF, bool DBG>
 __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves_per_eu(2))) gemm_kernel(
     Planes P, const int8_t *__restrict__ xq, const float *__restrict__ xs, const int *__restrict__ sx,
     float *__restrict__ out, int M, int N, int G, int mtiles, int ntiles, int splits, int sps,
@@ -412,24 +431,51 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
 
     if (threadIdx.x == 0) stages[0].tag = stages[1].tag = -1;
     __syncthreads();
-    Fetch<FMT, KB, BM, BN, T> f;
-    if (st0 < st1) {
-        fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
-        store_stage<FMT, KB, BM, BN, T>(f, stages[0], st0);
-    }
-    __syncthreads();
-
-    for (int s = st0; s < st1; s++) {
-        if (s + 1 < st1) fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * KB);
-        const St &S = stages[(s - st0) & 1];
-        if (S.tag != s)
-            stage_fast<FMT, KB, BM, BN, CF, KB / WK, WK, DBG>(S, wk, wm, wn, lane, cmag, acc, dots, m0, n0, M, N, G,
-                                                              s * KB);
+    auto compute = [&](int st) {
+        const St &S = stages[(st - st0) & 1];
+        if (S.tag != st)
+            stage_fast<FMT, KB, BM, BN, CF, KB / WK, WK, PIPE, DBG>(S, wk, wm, wn, lane, cmag, acc, dots, m0, n0, M,
+                                                                    N, G, st * KB);
         else
             stage_slow<FMT, KB, BM, BN, CF, KB / WK, WK, DBG>(S, wk, wm, wn, lane, cmag, acc, dots, m0, n0, M, N, G,
-                                                              s * KB);
-        if (s + 1 < st1) store_stage<FMT, KB, BM, BN, T>(f, stages[(s + 1 - st0) & 1], s + 1);
+                                                              st * KB);
+    };
+    using Fe = Fetch<FMT, KB, BM, BN, T>;
+    if (PF == 1) {
+        Fe f;
+        if (st0 < st1) {
+            fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
+            store_stage<FMT, KB, BM, BN, T>(f, stages[0], st0);
+        }
         __syncthreads();
+        for (int s = st0; s < st1; s++) {
+            if (s + 1 < st1) fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * KB);
+            compute(s);
+            if (s + 1 < st1) store_stage<FMT, KB, BM, BN, T>(f, stages[(s + 1 - st0) & 1], s + 1);
+            __syncthreads();
+        }
+    } else {
+        // two fetch register sets, filled alternately two stages ahead
+        Fe fa, fb;
+        if (st0 < st1) {
+            fetch_stage<FMT, KB, BM, BN, T>(fa, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
+            if (st0 + 1 < st1) fetch_stage<FMT, KB, BM, BN, T>(fb, P, xq, xs, sx, m0, n0, M, N, G, (st0 + 1) * KB);
+            store_stage<FMT, KB, BM, BN, T>(fa, stages[0], st0);
+        }
+        __syncthreads();
+        for (int s = st0; s < st1; s += 2) {
+            // stage s: fb holds stage s + 1
+            if (s + 2 < st1) fetch_stage<FMT, KB, BM, BN, T>(fa, P, xq, xs, sx, m0, n0, M, N, G, (s + 2) * KB);
+            compute(s);
+            if (s + 1 < st1) store_stage<FMT, KB, BM, BN, T>(fb, stages[(s + 1 - st0) & 1], s + 1);
+            __syncthreads();
+            if (s + 1 >= st1) break;
+            // stage s + 1: fa holds stage s + 2
+            if (s + 3 < st1) fetch_stage<FMT, KB, BM, BN, T>(fb, P, xq, xs, sx, m0, n0, M, N, G, (s + 3) * KB);
+            compute(s + 1);
+            if (s + 2 < st1) store_stage<FMT, KB, BM, BN, T>(fa, stages[(s + 2 - st0) & 1], s + 2);
+            __syncthreads();
+        }
     }
 
     // add the WK partial tiles: wk + step into wk, step = WK/2 .. 1 (fixed tree order)
@@ -640,10 +686,12 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
     }
 }
 
-// Workgroup shapes of the int8 GEMM: (waves along M, along N, along K, blocks per stage).
-// kWide: 64 x 128 tiles, 4 waves of 32 x 64; kDeep: 64 x 64 tiles, 4 waves of
-// 32 x 64, two of which take alternate blocks of each K stage. 4-block stages.
-enum GemmShape { kWide = 0, kDeep = 1 };
+// Workgroup shapes of the int8 GEMM (4 waves of 32 x 64, 4-block K stages).
+// kWide: 64 x 128 tiles, the blocks of a stage software-pipelined, one stage
+// of global loads in flight. kDeep: 64 x 64 tiles, two waves per 32 x 64
+// taking alternate blocks of each stage, pipelined. kDeepS: kDeep computing
+// one block at a time, two stages of global loads in flight.
+enum GemmShape { kWide = 0, kDeep = 1, kDeepS = 2 };
 
 struct GemmPlan {
     int shape, bn, kb, splits, sps, mtiles, ntiles;
@@ -663,7 +711,7 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
 }
 
 constexpr int kGemmBM = 64;
-constexpr int shape_bn(int fmt, int shape) { return shape == kDeep ? 64 : 128; }
+constexpr int shape_bn(int fmt, int shape) { return shape == kWide ? 128 : 64; }
 constexpr int shape_kb(int shape) { return 4; }
 
 GemmPlan plan_gemm(int fmt, int M, int N, int G) {
@@ -671,14 +719,13 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     const int cus = 256;
     GemmPlan p{};
     // Q5K1 (two MFMAs and a longer epilogue per block, so twice the registers
-    // per output) on the narrow tiles whose waves split each K stage; the other
-    // formats on the wide ones. Measured on C3 / C4 shapes at M = 64, 128, 512:
-    // wide Q4_1 14336x4096 36 / 57 / 173 us against 41 / 62 / 212 narrow, Q8_0
-    // 4096x14336 37 / 54 / 150 against 37 / 59 / 180; Q5K1 14336x4096 narrow
-    // 59 / 95 / 311 against 100 / 167 / 577 wide (its wide tiles spill).
-    p.shape = fmt == SLLM_Q5K1 ? kDeep : kWide;
-    if (tuning().gemm_shape == 1) p.shape = kWide;
-    if (tuning().gemm_shape == 2 && G % shape_kb(kDeep) == 0) p.shape = kDeep;
+    // per output) on the narrow tiles, the other formats on the wide ones.
+    // Measured at M = 64 / 128 / 512 (us): Q4_1 14336x4096 wide 37 / 57 / 172,
+    // deep 41 / 62 / 212; Q8_0 4096x14336 wide 37 / 52 / 148, deep 39 / 59 /
+    // 180; Q5K1 14336x4096 kDeepS 52 / 85 / 276, kDeep 54 / 84 / 306, wide
+    // 100 / 168 / 575 (its wide tiles spill).
+    p.shape = fmt == SLLM_Q5K1 ? kDeepS : kWide;
+    if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 3) p.shape = tuning().gemm_shape - 1;
     p.bn = shape_bn(fmt, p.shape);
     p.kb = shape_kb(p.shape);
     p.mtiles = (M + kGemmBM - 1) / kGemmBM;
@@ -693,7 +740,7 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     return p;
 }
 
-template <int FMT, int WM, int WN, int CF, int WK, int KB, bool DBG>
+template <int FMT, int WM, int WN, int CF, int WK, int KB, bool PIPE, int PF, bool DBG>
 sllm_status launch_shape(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
                          int N, int G, const GemmPlan &p, int *dots, hipStream_t s) {
     const int total = p.mtiles * p.ntiles * p.splits;
@@ -702,7 +749,7 @@ sllm_status launch_shape(const Planes &P, const int8_t *xq, const float *xsp, co
     constexpr size_t red = (size_t)(WK / 2) * WM * WN * 16 * CF * 64 * sizeof(float);
     constexpr size_t lds = stages > red ? stages : red;
     static_assert(lds <= 160 * 1024, "LDS");
-    hipLaunchKernelGGL((gemm_kernel<FMT, WM, WN, CF, WK, KB, DBG>), dim3(grid), dim3(64 * WM * WN * WK), lds, s, P, xq,
+    hipLaunchKernelGGL((gemm_kernel<FMT, WM, WN, CF, WK, KB, PIPE, PF, DBG>), dim3(grid), dim3(64 * WM * WN * WK), lds, s, P, xq,
                        xsp, sxp, out, M, N, G, p.mtiles, p.ntiles, p.splits, p.sps, dots);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
@@ -711,8 +758,11 @@ sllm_status launch_shape(const Planes &P, const int8_t *xq, const float *xsp, co
 template <int FMT, bool DBG>
 sllm_status launch_fmt(const Planes &P, const int8_t *xq, const float *xsp, const int *sxp, float *out, int M,
                        int N, int G, const GemmPlan &p, int *dots, hipStream_t s) {
-    if (p.shape == kDeep) return launch_shape<FMT, 2, 1, 2, 2, 4, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
-    return launch_shape<FMT, 2, 2, 2, 1, 4, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    switch (p.shape) {
+    case kDeep: return launch_shape<FMT, 2, 1, 2, 2, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case kDeepS: return launch_shape<FMT, 2, 1, 2, 2, 4, false, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    default: return launch_shape<FMT, 2, 2, 2, 1, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    }
 }
 
 template <bool DBG>

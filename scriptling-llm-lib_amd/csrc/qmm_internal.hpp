@@ -259,8 +259,7 @@ struct Tuning {
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
-    int gemm_shape = 0;        // GEMM workgroup shape: 1 wide (64 x 128 tiles), 2 deep (64 x 64, K split
-                               // over two waves); 0: by row count
+    int gemm_shape = 0;        // GEMM workgroup shape (1..3; 0: by format)
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
     int gemv_q6k_stream = 0;   // Q6_K weights: load (and stream) the native 6-bit planes (1) or the Q8_0 planes only (0)

@@ -43,11 +43,12 @@ def test_prefill_parity(qtype, M, N, K):
 
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
-@pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1)])
+@pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1), (3, 1), (3, 3), (3, 8)])
 def test_shape_and_split_overrides(qtype, shape, splits):
-    # either workgroup shape and any K split count gives the oracle's result
-    # within the bound (K = 1024 is 8 or 16 stages: 5 splits leave the last
-    # split empty on the 4-block stages, and it adds a zero tile)
+    # every workgroup shape and any K split count gives the oracle's result
+    # within the bound (K = 1024 is 8 stages: 5 splits of 2 stages leave the
+    # last split empty, and it adds a zero tile; 3 splits of 3 stages end on
+    # an odd stage count, which the two-stage prefetch handles)
     N, K, M = 320, 1024, 130
     raw = make_raw(qtype, N, K, seed=shape * 10 + splits)
     x = make_x(M, K, seed=splits)
@@ -80,7 +81,7 @@ def _block_dots_case(qtype, raw, N, K, x, row0, n_rows, shape=0):
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
 @pytest.mark.parametrize("M", [64, 130])
-@pytest.mark.parametrize("shape", [1, 2])
+@pytest.mark.parametrize("shape", [1, 2, 3])
 def test_gemm_block_dots_bitexact(qtype, M, shape):
     # the int32 block dots the matrix cores return, read from the registers the
     # epilogue scales, against the oracle's per-(row, block) dots
