@@ -381,25 +381,25 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
             r["dense_fp32_equiv_GBps"] = round(4.0 * N * K / (r["us"] * 1e-6) / 1e9, 1)
             table[f"{name} native {N}x{K} M=1"] = r
             del ws
-    # Q6_K streamed from its 6-bit codes (opt-in: tuning knob gemv_q6k_stream):
-    # the C3 down and the output head, the same weights timed streamed and from
-    # their Q8_0 planes (us_q8_planes)
-    sq.set_param("gemv_q6k_stream", 1)
-    try:
-        for N, K, seed in ((H, F, 102), (128256, H, 204)):
-            raw = synth.q6k_blocks(seed, N, K)
+    # Q6_K streamed from its 6-bit codes (opt-in: load option gemv_q6k_stream):
+    # the C3 down and the output head, the same blocks timed streamed and from
+    # weights loaded without the option (us_q8_planes)
+    for N, K, seed in ((H, F, 102), (128256, H, 204)):
+        raw = synth.q6k_blocks(seed, N, K)
+        sq.set_param("gemv_q6k_stream", 1)
+        try:
             w0 = sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K)
             n = int(min(64, max(2, -(-ROTATE_BYTES // w0.plane_bytes))))
             ws = [w0] + [sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K) for _ in range(n - 1)]
-            r = run(ws, 1, 100)
+        finally:
             sq.set_param("gemv_q6k_stream", 0)
-            rq = run(ws, 1, 100)
-            sq.set_param("gemv_q6k_stream", 1)
-            r.update({"us_q8_planes": rq["us"], "fp64_blocks": ws[0].q6k_exact_blocks})
-            table[f"q6k streamed {N}x{K} M=1 (opt-in)"] = r
-            del ws
-    finally:
-        sq.set_param("gemv_q6k_stream", 0)
+        r = run(ws, 1, 100)
+        r["fp64_blocks"] = ws[0].q6k_exact_blocks
+        del ws
+        wq = copies(lambda: sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K))
+        r["us_q8_planes"] = run(wq, 1, 100)["us"]
+        del wq
+        table[f"q6k streamed {N}x{K} M=1 (opt-in)"] = r
     torch.cuda.empty_cache()
     return table
 

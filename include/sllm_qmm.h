@@ -125,20 +125,25 @@ sllm_status sllm_weight_info(const sllm_weight *w, int *qtype, int *groups, int 
 
 /*
  * Bytes one decode GEMV of this weight streams from HBM (its planes as the
- * kernel reads them: the algorithmic weight bytes of a matmul). With the
- * tuning knob "gemv_q4k_stream" set, Q4_K weights stream the Q4_1 nibbles
- * and the GGUF Q4_K headers, 18 B per 32 weights (the Q4_1 scale and min
- * rebuilt in the kernel as convertQ4KToQ41 computes them,
- * kquant_kernels.go:30-63); by default they stream the Q4_1 planes (20 B),
- * which measures faster. No counterpart in the reference.
+ * kernel reads them: the algorithmic weight bytes of a matmul). Q4_K weights
+ * loaded while the load option "gemv_q4k_stream" is set keep the GGUF Q4_K
+ * headers beside the Q4_1 planes (2 B more per 256 weights) and their decode
+ * GEMV streams the Q4_1 nibbles and the headers, 18 B per 32 weights,
+ * rebuilding each block's Q4_1 scale and min as convertQ4KToQ41 computes
+ * them (kquant_kernels.go:30-63); other Q4_K weights stream the Q4_1 planes
+ * (20 B), which measures faster (C3 gate + up: 15.7-16.6 against 14.2-14.6
+ * us). No counterpart in the reference.
  */
 sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes);
 
 /*
- * GGUF Q6_K weights loaded while the tuning knob "gemv_q6k_stream" is set
- * keep their 6-bit codes beside the Q8_0 planes (28.25 B per 32 weights,
- * against 34), and while the knob is set the decode GEMV streams those and
- * rebuilds the Q8_0 codes and scale in registers, bit-identical to the Q8_0
+ * GGUF Q6_K weights loaded while the load option "gemv_q6k_stream" is set
+ * keep their 6-bit codes beside the Q8_0 planes, so such a weight holds both
+ * plane sets (about 62 B per 32 weights, 83 % more device memory than the
+ * Q8_0 planes alone); for the life of the weight its decode GEMV streams the
+ * 6-bit planes (28.25 B per 32 weights, against 34) and rebuilds the Q8_0
+ * codes and scale in registers (VALU-bound: C3 down 24.2 against 12.4 us,
+ * the 128256 x 4096 head 136 against 85 us), bit-identical to the Q8_0
  * planes the reference's load computes (dequantizeQ6KBlock + quantizeQ8Rows,
  * gguf.go:988-1015, 1080-1134). *blocks: the 32-element blocks it recomputes
  * with the reference's fp64 arithmetic (where the fast per-sub-block rule
@@ -403,9 +408,15 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
  *   gemv_wg_per_cu      1..8       GEMV workgroups per CU (1)
  *   gemv_max_nb         1..8       most 32-element blocks per lane per unit (8)
  *   gemv_inflight_kb    >= 64      weight bytes in flight over the device (32768)
- *   gemv_q4k_stream     0, 1       Q4_K weights streamed from their own headers (0)
- *   gemv_q6k_stream     0, 1       Q6_K weights loaded with, and streamed from, their
- *                                  6-bit codes (0; see sllm_weight_q6k_exact_blocks)
+ *   gemv_q4k_stream     0, 1       load option: Q4_K weights created while it is 1 keep
+ *                                  their GGUF headers and their GEMV streams them (0; see
+ *                                  sllm_weight_stream_bytes)
+ *   gemv_q6k_stream     0, 1       load option: Q6_K weights created while it is 1 keep
+ *                                  their 6-bit codes and their GEMV streams them (0; see
+ *                                  sllm_weight_q6k_exact_blocks)
+ *                                  (a weight's plane layout, and so its GEMV kernel, is
+ *                                  fixed when it is created: these two never act on the
+ *                                  call path)
  *   gemm_min_rows       >= 1       activation rows from which the GEMM is used (64;
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)

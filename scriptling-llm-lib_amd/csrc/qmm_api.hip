@@ -445,12 +445,11 @@ bool uses_gemm(const sllm_weight *w, int x_rows) {
     return x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups);
 }
 
-// The GEMV kernel format of a weight: Q4_K weights stream their GGUF headers
-// and Q6_K weights loaded with their native planes stream those, while the
-// tuning knob of each says so; every other weight its QType's planes.
+// The GEMV kernel format of a weight, fixed by its plane layout at load: Q4_K
+// / Q6_K weights loaded with their native planes stream those, every other
+// weight its QType's planes.
 int gemv_fmt(const sllm_weight *w) {
-    if (w->layout == SLLM_Q4K_STREAM && tuning().gemv_q4k_stream) return SLLM_Q4K_STREAM;
-    if (w->layout == SLLM_Q6K_STREAM && tuning().gemv_q6k_stream) return SLLM_Q6K_STREAM;
+    if (w->layout == SLLM_Q4K_STREAM || w->layout == SLLM_Q6K_STREAM) return w->layout;
     return w->fmt;
 }
 
@@ -764,7 +763,10 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     case 2: fmt = SLLM_Q4_0; per = 18; break;
     case 3: fmt = SLLM_Q4_1; per = 20; break;
     case 6: fmt = SLLM_Q5_0; per = 22; break;
-    case 12: fmt = SLLM_Q4_1; per = 144; blk = 256; layout = SLLM_Q4K_STREAM; break;
+    case 12:
+        fmt = SLLM_Q4_1; per = 144; blk = 256;
+        if (tuning().gemv_q4k_stream) layout = SLLM_Q4K_STREAM;
+        break;
     case 13: fmt = SLLM_Q5K1; per = 176; blk = 256; break;
     case 14:
         fmt = SLLM_Q8_0; per = 210; blk = 256;

@@ -261,8 +261,8 @@ struct Tuning {
     int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
     int gemm_shape = 0;        // GEMM workgroup shape (1..3; 0: by format)
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
-    int gemv_q4k_stream = 0;   // GEMV of Q4_K weights: stream the GGUF headers (1) or the Q4_1 scales (0, faster)
-    int gemv_q6k_stream = 0;   // Q6_K weights: load (and stream) the native 6-bit planes (1) or the Q8_0 planes only (0)
+    int gemv_q4k_stream = 0;   // load option: Q4_K weights keep (and stream) the GGUF headers (1) or not (0, faster)
+    int gemv_q6k_stream = 0;   // load option: Q6_K weights keep (and stream) the native 6-bit planes (1) or not (0)
     int attn_target_blocks = 512;  // attention: splits chosen to give about this many workgroups
     int attn_tile_groups = 4;      // attention: most tile groups (of max(4, rep) waves) per workgroup
     int attn_head_slices = 0;      // attention: workgroups sharing one kv head's q heads (0: by workgroup count)

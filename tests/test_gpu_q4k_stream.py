@@ -1,11 +1,12 @@
-"""GPU tests of Q4_K weights streamed natively (tuning knob gemv_q4k_stream;
-off by default: measured slower): the decode GEMV reads the Q4_1 nibble plane
-and the GGUF Q4_K header per super-block (18 B / 32 weights) and rebuilds each
-block's Q4_1 scale and min as convertQ4KToQ41 (kquant_kernels.go:30-63) does.
-Its results must be bit-identical to the kernel that reads the d / m planes
-the load-time remap wrote (which tests/test_gpu_parity.py pins to the oracle
-byte for byte), on every entry point, including headers with f16 special
-values."""
+"""GPU tests of Q4_K weights streamed natively (load option gemv_q4k_stream;
+off by default: measured slower): a Q4_K weight loaded with the option keeps
+the GGUF Q4_K header beside the Q4_1 planes, and its decode GEMV reads the Q4_1
+nibble plane and the headers (18 B / 32 weights), rebuilding each block's Q4_1
+scale and min as convertQ4KToQ41 (kquant_kernels.go:30-63) does. Its results
+are checked against the oracle (oracle.matmul over the Q4_1 Raw the reference's
+load computes) and must be bit-identical to those of the same weight loaded
+without the option (the Q4_1-plane kernel), on every entry point, including
+headers with f16 special values."""
 from __future__ import annotations
 
 import numpy as np
@@ -16,21 +17,22 @@ import oracle
 import sllm_qmm as sq
 from sllm_qmm import synth
 
-from _helpers import make_x
+from _helpers import assert_fp32_parity, make_x, term_abs_sum
 
 pytestmark = pytest.mark.gpu
 
 
-def _both(fn):
-    """fn() run with the streamed kernel and with the plane kernel."""
+def _load(raw: np.ndarray, N: int, K: int, stream: bool) -> sq.DeviceWeight:
+    sq.set_param("gemv_q4k_stream", int(stream))
     try:
-        sq.set_param("gemv_q4k_stream", 1)
-        a = fn()
-        sq.set_param("gemv_q4k_stream", 0)
-        b = fn()
+        return sq.load_weight_f32_direct(synth.GGML_Q4_K, raw, N, K)
     finally:
         sq.set_param("gemv_q4k_stream", 0)  # the default
-    return a, b
+
+
+def _pair(raw: np.ndarray, N: int, K: int):
+    """The weight loaded with its headers (streamed) and without (Q4_1 planes)."""
+    return _load(raw, N, K, True), _load(raw, N, K, False)
 
 
 def _bits(t):
@@ -48,36 +50,45 @@ def _special_headers(raw: np.ndarray) -> np.ndarray:
 
 
 @pytest.mark.parametrize("N,K,M", [(14336, 4096, 1), (4096, 14336, 1), (300, 1024, 3), (37, 2048, 5)])
-def test_stream_equals_planes(N, K, M):
+def test_stream_equals_planes_and_oracle(N, K, M):
     raw = synth.q4k_blocks(70 + M, N, K)
-    w = sq.load_weight_f32_direct(synth.GGML_Q4_K, raw, N, K)
+    ws, wp = _pair(raw, N, K)
+    assert ws.plane_bytes == N * K // 32 * 18 and wp.plane_bytes == N * K // 32 * 20
     x = make_x(M, K, seed=M)
-    a, b = _both(lambda: sq.model_matmul_quant_into_f32(w, x, M, K)[0].copy())
+    a = sq.model_matmul_quant_into_f32(ws, x, M, K)[0].copy()
+    b = sq.model_matmul_quant_into_f32(wp, x, M, K)[0].copy()
     assert np.array_equal(_bits(a), _bits(b))
-    # the plane kernel's result is the oracle's path (Q4_1 after convertQ4KToQ41)
+    # the streamed kernel against the oracle directly (Q4_1 after convertQ4KToQ41)
     qt, q41 = oracle.load_weight(12, raw, N, K)
-    assert qt == "q4_1" and np.array_equal(w.export(), q41)
+    assert qt == "q4_1" and np.array_equal(ws.export(), q41) and np.array_equal(wp.export(), q41)
+    ref = oracle.matmul("q4_1", q41, N, x)
+    assert_fp32_parity(a.reshape(M, N), ref, term_abs_sum("q4_1", q41, N, x), f"q4k stream {N}x{K} M={M}")
 
 
 def test_special_header_values():
     N, K = 64, 2048
     raw = _special_headers(synth.q4k_blocks(5, N, K))
-    w = sq.load_weight_f32_direct(synth.GGML_Q4_K, raw, N, K)
-    assert np.array_equal(w.export(), oracle.load_weight(12, raw, N, K)[1])
+    ws, wp = _pair(raw, N, K)
+    q41 = oracle.load_weight(12, raw, N, K)[1]
+    assert np.array_equal(ws.export(), q41)
     x = make_x(2, K, seed=6)
-    a, b = _both(lambda: sq.model_matmul_quant_into_f32(w, x, 2, K)[0].copy())
+    a = sq.model_matmul_quant_into_f32(ws, x, 2, K)[0].copy()
+    b = sq.model_matmul_quant_into_f32(wp, x, 2, K)[0].copy()
     assert np.array_equal(_bits(a), _bits(b))
+    assert_fp32_parity(a.reshape(2, N), oracle.matmul("q4_1", q41, N, x), term_abs_sum("q4_1", q41, N, x),
+                       "q4k stream special headers")
 
 
 def test_stream_on_fused_entries_and_bytes():
     H, F = 4096, 1536
-    g = sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(80, F, H), F, H)
-    u = sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(81, F, H), F, H)
+    g_raw, u_raw = synth.q4k_blocks(80, F, H), synth.q4k_blocks(81, F, H)
+    gs, gp = _pair(g_raw, F, H)
+    us, up = _pair(u_raw, F, H)
     x = torch.from_numpy(make_x(1, H, seed=9)).cuda()
     nw = torch.from_numpy(np.random.default_rng(3).normal(1, 0.1, H).astype(np.float32)).cuda()
     P = lambda t: t.data_ptr()
 
-    def run():
+    def run(g, u):
         h = torch.empty(F, device="cuda")
         o = [torch.empty(F, device="cuda") for _ in range(2)]
         idx = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -87,13 +98,15 @@ def test_stream_on_fused_entries_and_bytes():
         torch.cuda.synchronize()
         return h.clone(), o[0].clone(), o[1].clone(), int(idx.item())
 
-    a, b = _both(run)
+    a, b = run(gs, us), run(gp, up)
     for ta, tb in zip(a[:3], b[:3]):
         assert torch.equal(ta.view(torch.int32), tb.view(torch.int32))
     assert a[3] == b[3]
-    assert g.plane_bytes == F * H // 32 * 20  # default: the Q4_1 planes
+    # the option acts at load only: it never changes an existing weight's kernel
     sq.set_param("gemv_q4k_stream", 1)
     try:
-        assert g.plane_bytes == F * H // 32 * 18
+        assert gp.plane_bytes == F * H // 32 * 20 and gs.plane_bytes == F * H // 32 * 18
+        c = run(gs, us)
     finally:
         sq.set_param("gemv_q4k_stream", 0)
+    assert all(torch.equal(ta.view(torch.int32), tc.view(torch.int32)) for ta, tc in zip(a[:3], c[:3]))

@@ -1,13 +1,14 @@
-"""GPU tests of Q6_K weights streamed natively (tuning knob gemv_q6k_stream,
-off by default). A Q6_K weight loaded with the knob set keeps its 6-bit codes
+"""GPU tests of Q6_K weights streamed natively (load option gemv_q6k_stream,
+off by default). A Q6_K weight loaded with the option keeps its 6-bit codes
 beside the Q8_0 planes the reference's load computes (dequantizeQ6KBlock +
-quantizeQ8Rows, gguf.go:988-1015, 1080-1134), and the decode GEMV, while the
-knob is set, rebuilds each block's Q8_0 codes and scale in registers from
-them. Its results must be bit-identical to the kernel that reads the Q8_0
-planes (which tests/test_gpu_parity.py pins to the oracle byte for byte), on
-every entry point: random blocks, blocks built to have exact ties that round
-both ways inside one sub-block (left to the kernel's fp64 path), and f16
-special values of d."""
+quantizeQ8Rows, gguf.go:988-1015, 1080-1134), and its decode GEMV rebuilds
+each block's Q8_0 codes and scale in registers from them. Its results are
+checked against the oracle (oracle.matmul over the requantized Q8_0 Raw) and
+must be bit-identical to those of the same weight loaded without the option
+(the Q8_0-plane kernel), on every entry point: random blocks, blocks built to
+have exact ties that round both ways inside one sub-block (left to the
+kernel's fp64 path), f16 special values of d, and the full 128256 x 4096
+head."""
 from __future__ import annotations
 
 import numpy as np
@@ -18,30 +19,30 @@ import oracle
 import sllm_qmm as sq
 from sllm_qmm import synth
 
-from _helpers import make_x
+from _helpers import assert_fp32_parity, make_x, term_abs_sum
 
 pytestmark = pytest.mark.gpu
 
 
-def _load(raw: np.ndarray, N: int, K: int) -> sq.DeviceWeight:
-    """A Q6_K weight loaded with its streamed planes."""
-    sq.set_param("gemv_q6k_stream", 1)
+def _load(raw: np.ndarray, N: int, K: int, stream: bool = True) -> sq.DeviceWeight:
+    """A Q6_K weight loaded with (stream) or without its streamed planes."""
+    sq.set_param("gemv_q6k_stream", int(stream))
     try:
         return sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K)
     finally:
-        sq.set_param("gemv_q6k_stream", 0)
-
-
-def _both(fn):
-    """fn() run with the streamed kernel and with the Q8_0-plane kernel."""
-    try:
-        sq.set_param("gemv_q6k_stream", 1)
-        a = fn()
-        sq.set_param("gemv_q6k_stream", 0)
-        b = fn()
-    finally:
         sq.set_param("gemv_q6k_stream", 0)  # the default
-    return a, b
+
+
+def _pair(raw: np.ndarray, N: int, K: int):
+    """The weight loaded with its 6-bit planes (streamed) and without (Q8_0 planes)."""
+    return _load(raw, N, K, True), _load(raw, N, K, False)
+
+
+def _check_oracle(got: np.ndarray, raw_q8: np.ndarray, N: int, x: np.ndarray, what: str) -> None:
+    """The streamed kernel's output against the oracle (Q8_0 after the reference's requantization)."""
+    x = np.asarray(x, np.float32).reshape(-1, x.shape[-1])
+    assert_fp32_parity(np.asarray(got).reshape(x.shape[0], N), oracle.matmul("q8", raw_q8, N, x),
+                       term_abs_sum("q8", raw_q8, N, x), what)
 
 
 def _bits(t):
@@ -97,26 +98,31 @@ def test_tie_blocks_decode_like_the_reference():
     # the load-time planes are the oracle's; exact ties in both directions exist
     N, K = 64, 2048
     raw = _tie_blocks(1, N, K)
-    w = _load(raw, N, K)
+    ws, wp = _pair(raw, N, K)
     qt, ref = oracle.load_weight(14, raw, N, K)
-    assert qt == "q8" and np.array_equal(w.export(), ref)
-    assert 0 < w.q6k_exact_blocks < N * K // 32  # some blocks need the fp64 path, most do not
+    assert qt == "q8" and np.array_equal(ws.export(), ref)
+    assert 0 < ws.q6k_exact_blocks < N * K // 32  # some blocks need the fp64 path, most do not
     for M in (1, 2, 5):
         x = make_x(M, K, seed=M)
-        a, b = _both(lambda: sq.model_matmul_quant_into_f32(w, x, M, K)[0].copy())
+        a = sq.model_matmul_quant_into_f32(ws, x, M, K)[0].copy()
+        b = sq.model_matmul_quant_into_f32(wp, x, M, K)[0].copy()
         assert np.array_equal(_bits(a), _bits(b)), f"M={M}"
+        _check_oracle(a, ref, N, x, f"tie blocks M={M}")
 
 
-@pytest.mark.parametrize("N,K,M", [(4096, 14336, 1), (300, 1024, 3), (37, 2048, 5), (128, 4096, 4)])
-def test_stream_equals_planes(N, K, M):
+@pytest.mark.parametrize("N,K,M", [(4096, 14336, 1), (14336, 4096, 1), (300, 1024, 3), (37, 2048, 5),
+                                   (128, 4096, 4)])
+def test_stream_equals_planes_and_oracle(N, K, M):
     raw = synth.q6k_blocks(90 + M, N, K)
-    w = _load(raw, N, K)
+    ws, wp = _pair(raw, N, K)
     x = make_x(M, K, seed=M + 1)
-    a, b = _both(lambda: sq.model_matmul_quant_into_f32(w, x, M, K)[0].copy())
+    a = sq.model_matmul_quant_into_f32(ws, x, M, K)[0].copy()
+    b = sq.model_matmul_quant_into_f32(wp, x, M, K)[0].copy()
     assert np.array_equal(_bits(a), _bits(b))
-    assert w.q6k_exact_blocks >= 0
-    if N * K <= 1 << 22:
-        assert np.array_equal(w.export(), oracle.load_weight(14, raw, N, K)[1])
+    assert ws.q6k_exact_blocks >= 0
+    ref = oracle.load_weight(14, raw, N, K)[1]
+    assert np.array_equal(ws.export(), ref)
+    _check_oracle(a, ref, N, x, f"q6k stream {N}x{K} M={M}")
 
 
 def test_special_d_values():
@@ -128,42 +134,44 @@ def test_special_d_values():
     raw[3, 192:208] = 0            # every scale zero: Mi = 0
     raw[5, 192:208] = 0x80         # every scale -128
     raw = raw.reshape(-1)
-    w = _load(raw, N, K)
-    assert np.array_equal(w.export(), oracle.load_weight(14, raw, N, K)[1])
+    ws, wp = _pair(raw, N, K)
+    ref = oracle.load_weight(14, raw, N, K)[1]
+    assert np.array_equal(ws.export(), ref)
     x = make_x(3, K, seed=4)
-    a, b = _both(lambda: sq.model_matmul_quant_into_f32(w, x, 3, K)[0].copy())
+    a = sq.model_matmul_quant_into_f32(ws, x, 3, K)[0].copy()
+    b = sq.model_matmul_quant_into_f32(wp, x, 3, K)[0].copy()
     assert np.array_equal(_bits(a), _bits(b))
+    _check_oracle(a, ref, N, x, "q6k stream special d")
 
 
-def test_knob_off_at_load_keeps_q8_planes_only():
+def test_option_acts_at_load_only():
     N, K = 64, 1024
     raw = synth.q6k_blocks(3, N, K)
-    w = sq.load_weight_f32_direct(synth.GGML_Q6_K, raw, N, K)
-    assert w.q6k_exact_blocks == -1
-    sq.set_param("gemv_q6k_stream", 1)
-    try:
-        assert w.plane_bytes == N * K // 32 * 34  # no streamed planes: the Q8_0 kernel
-    finally:
-        sq.set_param("gemv_q6k_stream", 0)
-    s = _load(raw, N, K)
-    assert s.plane_bytes == N * K // 32 * 34
-    sq.set_param("gemv_q6k_stream", 1)
-    try:
-        assert s.plane_bytes == N * K // 32 * 28 + N * K // 256 * 2
-    finally:
-        sq.set_param("gemv_q6k_stream", 0)
+    ws, wp = _pair(raw, N, K)
+    assert wp.q6k_exact_blocks == -1 and ws.q6k_exact_blocks >= 0
+    x = make_x(2, K, seed=3)
+    a = sq.model_matmul_quant_into_f32(ws, x, 2, K)[0].copy()
+    for opt in (1, 0):
+        sq.set_param("gemv_q6k_stream", opt)
+        try:
+            assert wp.plane_bytes == N * K // 32 * 34  # no streamed planes: the Q8_0 kernel
+            assert ws.plane_bytes == N * K // 32 * 28 + N * K // 256 * 2
+            assert np.array_equal(_bits(sq.model_matmul_quant_into_f32(ws, x, 2, K)[0]), _bits(a))
+        finally:
+            sq.set_param("gemv_q6k_stream", 0)
 
 
 def test_stream_on_fused_entries():
     H, F = 4096, 1536
-    g = _load(synth.q6k_blocks(80, F, H), F, H)
-    u = _load(_tie_blocks(81, F, H), F, H)
+    g_raw, u_raw = synth.q6k_blocks(80, F, H), _tie_blocks(81, F, H)
+    gs, gp = _pair(g_raw, F, H)
+    us, up = _pair(u_raw, F, H)
     x = torch.from_numpy(make_x(1, H, seed=9)).cuda()
     nw = torch.from_numpy(np.random.default_rng(3).normal(1, 0.1, H).astype(np.float32)).cuda()
     res0 = torch.from_numpy(make_x(1, F, seed=10)).cuda()
     P = lambda t: t.data_ptr()
 
-    def run():
+    def run(g, u):
         h = torch.empty(F, device="cuda")
         o = [torch.empty(F, device="cuda") for _ in range(2)]
         idx = torch.zeros(1, dtype=torch.int32, device="cuda")
@@ -175,7 +183,7 @@ def test_stream_on_fused_entries():
         torch.cuda.synchronize()
         return h.clone(), o[0].clone(), o[1].clone(), r, int(idx.item())
 
-    a, b = _both(run)
+    a, b = run(gs, us), run(gp, up)
     for ta, tb in zip(a[:4], b[:4]):
         assert torch.equal(ta.view(torch.int32), tb.view(torch.int32))
     assert a[4] == b[4]
@@ -183,19 +191,27 @@ def test_stream_on_fused_entries():
 
 def test_head_rmsnorm_argmax_full_size():
     # the Llama-3-8B output head (128256 x 4096, Q6_K) through the fused head
-    # entry point, streamed and from the Q8_0 planes
+    # entry point, streamed and from the Q8_0 planes, and the streamed logits
+    # against the oracle's matmul of the same RMSNorm output
     N, H = 128256, 4096
-    w = _load(synth.q6k_blocks(55, N, H), N, H)
-    x = torch.from_numpy(make_x(1, H, seed=56)).cuda()
-    nw = torch.from_numpy(np.random.default_rng(57).normal(1, 0.1, H).astype(np.float32)).cuda()
+    raw = synth.q6k_blocks(55, N, H)
+    ws, wp = _pair(raw, N, H)
+    xh = make_x(1, H, seed=56)
+    nwh = np.random.default_rng(57).normal(1, 0.1, H).astype(np.float32)
+    x = torch.from_numpy(xh).cuda()
+    nw = torch.from_numpy(nwh).cuda()
 
-    def run():
+    def run(w):
         logits = torch.empty(N, device="cuda")
         idx = torch.zeros(1, dtype=torch.int32, device="cuda")
         sq.rmsnorm_matmul_argmax_dev(w, x.data_ptr(), nw.data_ptr(), 1e-5, idx.data_ptr(), logits.data_ptr())
         torch.cuda.synchronize()
         return logits.clone(), int(idx.item())
 
-    a, b = _both(run)
+    a, b = run(ws), run(wp)
     assert torch.equal(a[0].view(torch.int32), b[0].view(torch.int32))
     assert a[1] == b[1]
+    normed = oracle.rmsnorm(xh, nwh, 1e-5, lib_order=True).reshape(1, H)
+    ref_q8 = wp.export()
+    _check_oracle(a[0].cpu().numpy(), ref_q8, N, normed, "q6k stream head")
+    assert a[1] == oracle.argmax(oracle.matmul("q8", ref_q8, N, normed)[0])
