@@ -1,7 +1,9 @@
 """BASELINE config C5 (the decode step of a Llama-3-8B-shaped Q4_K_M model)
 as a teacher-forced parity harness: two full-width layers and the full Q6_K
-head, eight greedy tokens, through the device entry points bench.py's decode
-step uses (forwardBlock model_f32.go:382-500, outputLogits :502-527, the
+head, eight greedy tokens from an empty cache and two at cache positions 2046
+and 2047 (the cache pre-filled with 2046 seeded rows, the last position of the
+2048 context bench.py's decode step reports), through the device entry points
+bench.py's decode step uses (forwardBlock model_f32.go:382-500, outputLogits :502-527, the
 greedy loop :643-652). After every launch the GPU's output is compared with
 the oracle applied to the GPU's own inputs to that launch (teacher forcing),
 so each check carries only that launch's reassociation bound:
@@ -75,7 +77,9 @@ def _residual_check(x_in, got, wraw, qtype, n, inp, what):
     assert np.all(err <= bound), (what, float((err / bound).max()))
 
 
-def test_c5_teacher_forced_decode():
+def _run_c5(start: int, ntok: int) -> None:
+    """ntok teacher-forced greedy tokens at cache positions start .. start + ntok - 1;
+    rows [0, start) of every layer's cache hold seeded K ~ N(0, 0.5^2), V ~ N(0, 1)."""
     torch.cuda.set_device(0)
     mk = _load
     layers = []
@@ -104,8 +108,20 @@ def test_c5_teacher_forced_decode():
     for lw in layers:
         lw["n1d"], lw["n2d"] = dev(lw["n1"]), dev(lw["n2"])
     noutd = dev(nout)
-    cap = T + 4
+    cap = start + ntok + 4
     kvc = sq.KVCache(L, KVH, DK, cap)
+    if start:
+        rng = np.random.default_rng(4242)
+        for li in range(L):
+            kp, vp = kvc.data(li)
+            kc = np.zeros((KVH, cap, DK), np.float32)
+            vc = np.zeros((KVH, cap, DK), np.float32)
+            kc[:, :start] = rng.normal(0, 0.5, (KVH, start, DK))
+            vc[:, :start] = rng.normal(0, 1.0, (KVH, start, DK))
+            dev_view(kp, KVH * cap * DK).copy_(torch.from_numpy(kc.reshape(-1)))
+            dev_view(vp, KVH * cap * DK).copy_(torch.from_numpy(vc.reshape(-1)))
+        torch.cuda.synchronize()
+        kvc.set_length(start)
     x = torch.empty(H, device="cuda")
     q, k, v = torch.empty(H, device="cuda"), torch.empty(KVH * DK, device="cuda"), torch.empty(KVH * DK, device="cuda")
     att, h = torch.empty(H, device="cuda"), torch.empty(F, device="cuda")
@@ -115,7 +131,7 @@ def test_c5_teacher_forced_decode():
     host = lambda t: t.cpu().numpy().copy()
 
     tok, tokens = 1, []
-    for pos in range(T):
+    for pos in range(start, start + ntok):
         x.copy_(dev(_embed(tok)))
         for li, lw in enumerate(layers):
             (wq, rq), (wk, rk), (wv, rv) = lw["q"], lw["k"], lw["v"]
@@ -172,5 +188,15 @@ def test_c5_teacher_forced_decode():
         tokens.append(t)
         tok = t
         assert kvc.length(0) == kvc.length(L - 1) == pos + 1
-    print(f"C5 teacher-forced greedy tokens: {tokens}")
+    print(f"C5 teacher-forced greedy tokens at positions {start}..{start + ntok - 1}: {tokens}")
     kvc.close()
+
+
+def test_c5_teacher_forced_decode():
+    _run_c5(0, T)
+
+
+def test_c5_teacher_forced_decode_kv2047():
+    # the decode step at the end of the 2048 context (bench.py's
+    # decode_full_*_kv2047 lines): attention over 2047 and 2048 cached rows
+    _run_c5(2046, 2)
