@@ -53,8 +53,10 @@ struct Ctx {
     hipStream_t stream = nullptr;
     void *buf = nullptr;
     size_t cap = 0;
-    void *hbuf = nullptr;  // pinned host memory (hipHostMalloc)
+    void *hbuf = nullptr;  // pinned host memory (hipHostMalloc, cacheable by the GPU): inputs and copies
     size_t hcap = 0;
+    void *obuf = nullptr;  // coherent pinned host memory (kDirectOutBytes): outputs the kernels write directly
+
     unsigned *flag = nullptr;  // coherent pinned word: the stream writes seq there when a call's work is done
     unsigned seq = 0;
 };
@@ -63,10 +65,15 @@ std::vector<Ctx *> g_pool;
 // Host transfers of a call at most this large go through the context's
 // pinned bounce buffer (a host memcpy plus a DMA from / to pinned memory,
 // instead of the runtime staging pageable memory itself); larger ones are
-// copied from / to the caller's pageable memory directly.
+// copied from / to the caller's pageable memory directly. The buffer grows
+// geometrically up to this size, so each pooled context (one per caller
+// running concurrently on a device) holds at most kMaxPinnedBytes +
+// kDirectOutBytes of pinned host memory for the life of the process.
 constexpr size_t kMaxPinnedBytes = (size_t)64 << 20;
 // Outputs of a call at most this large (together) are written by the kernels
-// straight into the pinned buffer (device-visible host memory), without a
+// straight into the context's coherent pinned buffer (fine-grained host
+// memory: the kernels' stores reach host memory before the kernels complete,
+// so they are visible once the completion word below is), without a
 // device-to-host copy.
 constexpr size_t kDirectOutBytes = (size_t)1 << 20;
 // Inputs of at most this size are read by the kernels from the pinned bounce
@@ -210,14 +217,8 @@ sllm_status ensure_init() {
         g_init_msg = std::string("device is ") + prop.gcnArchName + ", this build targets gfx950 only";
         return set_error(g_init_status, g_init_msg);
     }
-    // the static scratch of the current device (other devices: at their first call)
-    void *scr = nullptr;
-    sllm_status st = static_scratch_locked(dev, &scr);
-    if (st != SLLM_OK) {
-        g_init_status = st;
-        g_init_msg = g_err;
-        return st;
-    }
+    // (the static scratch's address is looked up by the first no-allocation
+    // call on each device, whose error stays that call's)
     g_init_status = SLLM_OK;
     return SLLM_OK;
 }
@@ -307,13 +308,25 @@ bool pinned(Ctx *c, size_t bytes) {
     if (c->hcap >= bytes) return true;
     if (c->hbuf) (void)hipHostFree(c->hbuf);
     c->hbuf = nullptr;
+    size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+    if (want < 2 * c->hcap) want = 2 * c->hcap;  // geometric growth: rising sizes reallocate rarely
+    if (want > kMaxPinnedBytes) want = kMaxPinnedBytes;
     c->hcap = 0;
-    const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
     if (hipHostMalloc(&c->hbuf, want, hipHostMallocDefault) != hipSuccess) {
         c->hbuf = nullptr;
         return false;
     }
     c->hcap = want;
+    return true;
+}
+
+// The context's coherent output buffer (kDirectOutBytes), allocated once.
+bool coherent_out(Ctx *c) {
+    if (c->obuf) return true;
+    if (hipHostMalloc(&c->obuf, kDirectOutBytes, hipHostMallocCoherent) != hipSuccess) {
+        c->obuf = nullptr;
+        return false;
+    }
     return true;
 }
 
@@ -352,7 +365,7 @@ hipError_t wait_stream(Ctx *c) {
 // `launch` on the context's stream, bring the outputs back and wait for the
 // stream. Small transfers bounce through pinned memory; small inputs are read
 // by the kernels from the pinned buffer itself (no upload enqueue) and small
-// outputs are written there. launch(iaddr, oaddr) gets the device-visible
+// outputs are written into the coherent pinned buffer. launch(iaddr, oaddr) gets the device-visible
 // address each input is to be read from and each output is to be written to.
 struct HostIn {
     const void *src;
@@ -371,8 +384,9 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
     for (int i = 0; i < nout; i++) tout += (out[i].bytes + 255) & ~(size_t)255;
     const bool pin = pinned(c, tin + tout);
     const bool direct_in = pin && tin <= kDirectInBytes;
-    const bool direct = pin && tout <= kDirectOutBytes;
+    const bool direct = pin && tout <= kDirectOutBytes && coherent_out(c);
     char *hb = (char *)c->hbuf;
+    char *ob = (char *)c->obuf;
     hipError_t e = hipSuccess;
     size_t off = 0;
     void *i1[4];
@@ -389,14 +403,18 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
             e = hipMemcpyAsync(in[i].dev, in[i].src, in[i].bytes, hipMemcpyHostToDevice, c->stream);
         }
     }
-    if (e != hipSuccess) return hip_error(e, "host-to-device copy");
+    if (e != hipSuccess) {
+        (void)hipStreamSynchronize(c->stream);  // copies enqueued before the failure still read the bounce buffer
+        return hip_error(e, "host-to-device copy");
+    }
     const size_t obase = off;
     void *o1[4];  // the usual case; more outputs take a vector
     std::vector<void *> on(nout > 4 ? (size_t)nout : 0);
     void **oaddr = nout > 4 ? on.data() : o1;
+    size_t doff = 0;
     for (int i = 0; i < nout; i++) {
-        oaddr[i] = direct ? (void *)(hb + off) : out[i].dev;
-        off += (out[i].bytes + 255) & ~(size_t)255;
+        oaddr[i] = direct ? (void *)(ob + doff) : out[i].dev;
+        doff += (out[i].bytes + 255) & ~(size_t)255;
     }
     sllm_status st = launch((void *const *)iaddr, (void *const *)oaddr);
     if (st != SLLM_OK) {
@@ -416,9 +434,10 @@ sllm_status host_call(Ctx *c, const HostIn *in, int nin, const HostOut *out, int
     if (e == hipSuccess) e = es;
     if (e != hipSuccess) return hip_error(e, "device-to-host copy");
     if (pin) {
-        off = obase;
+        off = direct ? 0 : obase;
+        const char *src = direct ? ob : hb;
         for (int i = 0; i < nout; i++) {
-            std::memcpy(out[i].dst, hb + off, out[i].bytes);
+            std::memcpy(out[i].dst, src + off, out[i].bytes);
             off += (out[i].bytes + 255) & ~(size_t)255;
         }
     }
