@@ -288,9 +288,8 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
     Each entry rotates over copies of its weight totalling >= 1 GiB (at most
     512 copies, so C1's 0.9 MB weight can stay in the MALL: C1 is launch-bound
     at any rate). GEMV lines give GB/s of algorithmic bytes; GEMM lines (M >=
-    64) also give TOPS (2 M N K per call) against the int8 MFMA peak measured
-    on the box (the K = 64 form; the published 5.0 POPS when the probe did not
-    run), or for Q5_0 (fp32 activations, exact per-block sums on the VALU at 2
+    64) also give TOPS (2 M N K per call) against the published 5.0 POPS dense
+    int8 MFMA peak, or for Q5_0 (fp32 activations, exact per-block sums on the VALU at 2
     ops per MAC) against the 78.6 T lane-ops/s VALU peak. Q5_K rows stream 26 B / 32 weights (the two Q4_1 halves of
     convertQ5KToTwoQ41 without the high half's zero mins and 4-bit codes).
     M = 1 lines also give us_graph: the per-launch time of 100 of the same
@@ -334,9 +333,7 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
                 r.update({"TOPS": round(tops, 1), "frac_valu": round(tops / VALU_PEAK_TOPS, 4),
                           "path": "VALU GEMM (Q5_0 keeps fp32 activations)"})
             else:
-                pk = (peaks or {}).get("v_mfma_i32_16x16x64_i8") or INT8_MFMA_PEAK_TOPS
-                r.update({"TOPS": round(tops, 1), "frac_int8_mfma": round(tops / pk, 4),
-                          "frac_int8_mfma_spec": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                r.update({"TOPS": round(tops, 1), "frac_int8_mfma": round(tops / INT8_MFMA_PEAK_TOPS, 4),
                           "path": "int8 MFMA GEMM"})
         return r
 
@@ -784,12 +781,14 @@ def mfma_peaks() -> dict | None:
     L = C.CDLL(path)
     L.sllm_probe_mfma_tops.argtypes = [C.c_int, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double)]
     out = {}
-    for form, name in ((0, "v_mfma_i32_16x16x32_i8"), (1, "v_mfma_i32_16x16x64_i8")):
-        t = C.c_double()
-        if L.sllm_probe_mfma_tops(form, 4096, 2048, 5, C.byref(t)) == 0:
-            out[name] = round(t.value, 1)
-    out["note"] = ("4096 workgroups x 4 waves, 8 independent MFMA chains per wave, register operands only; the "
-                   "fastest of 5 launches")
+    for form, name in ((0, "v_mfma_i32_16x16x32_i8"), (1, "v_mfma_i32_16x16x64_i8"), (2, "v_mfma_i32_32x32x32_i8")):
+        for blocks in (1024, 4096):
+            t = C.c_double()
+            if L.sllm_probe_mfma_tops(form, blocks, 2048, 5, C.byref(t)) == 0:
+                out[f"{name} x{blocks}"] = round(t.value, 1)
+    out["note"] = ("1024 or 4096 workgroups x 4 waves (1 or 4 waves per SIMD), 8 independent MFMA chains per wave "
+                   "(4 for the 32x32 form), register operands only; the fastest of 5 launches. The GEMM lines' "
+                   "frac_int8_mfma is against the published 5.0 POPS dense figure, not against these.")
     return out
 
 

@@ -8,13 +8,16 @@
 //           (K = 32 is one Q8_0 block, so each result is one block's exact
 //           int32 dot);
 //   form 1: v_mfma_i32_16x16x64_i8 (gfx950), the form the published
-//           5.0 POPS dense int8 figure is quoted for.
+//           5.0 POPS dense int8 figure is quoted for;
+//   form 2: v_mfma_i32_32x32x32_i8 (gfx950), the instruction the prefill GEMM
+//           issues (K = 32 is one Q8_0 block, and the form runs at the full
+//           int8 rate).
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
 
 typedef int v4i __attribute__((ext_vector_type(4)));
-typedef long v1l __attribute__((ext_vector_type(1)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 namespace {
 
@@ -33,12 +36,28 @@ __global__ void __launch_bounds__(256) mfma_loop(v4i *out, int iters, int seed) 
 #pragma unroll
             for (int c = 0; c < kChains; c++) acc[c] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, acc[c], 0, 0, 0);
         }
-    } else {
+    } else if (FORM == 1) {
         const v4i a = {s, s + 1, s + 2, s + 3}, b = {s * 3, s * 5, s * 7, s * 9};
         for (int it = 0; it < iters; it++) {
 #pragma unroll
             for (int c = 0; c < kChains; c++) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
         }
+    } else {
+        // 32 x 32 results: 4 independent chains of 16 registers each
+        const v4i a = {s, s + 1, s + 2, s + 3}, b = {s * 3, s * 5, s * 7, s * 9};
+        v16i big[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) big[c][r] = 0;
+        for (int it = 0; it < iters; it++) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) big[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, big[c], 0, 0, 0);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[c][r] = big[c][r] ^ big[c][r + 4] ^ big[c][r + 8] ^ big[c][r + 12];
     }
     v4i t = acc[0];
 #pragma unroll
@@ -129,12 +148,12 @@ int sllm_probe_valu_rate(int op, int blocks, int iters, int reps, double *rate) 
     return 0;
 }
 
-// Runs `reps` launches of form `form` (0 or 1) over `blocks` workgroups of 4
+// Runs `reps` launches of form `form` (0, 1 or 2) over `blocks` workgroups of 4
 // waves, `iters` loop trips each, on the current device's null stream, and
 // returns the sustained rate in TOPS (2 x M x N x K per MFMA) of the fastest
 // launch in *tops. Returns 0 on success, else a hipError_t.
 int sllm_probe_mfma_tops(int form, int blocks, int iters, int reps, double *tops) {
-    if (!tops || blocks <= 0 || iters <= 0 || reps <= 0 || (form != 0 && form != 1)) return (int)hipErrorInvalidValue;
+    if (!tops || blocks <= 0 || iters <= 0 || reps <= 0 || form < 0 || form > 2) return (int)hipErrorInvalidValue;
     v4i *out = nullptr;
     hipError_t e = hipMalloc(&out, (size_t)blocks * 256 * sizeof(v4i));
     if (e != hipSuccess) return (int)e;
@@ -145,7 +164,8 @@ int sllm_probe_mfma_tops(int form, int blocks, int iters, int reps, double *tops
     for (int r = 0; r <= reps && e == hipSuccess; r++) {  // launch 0 warms up
         (void)hipEventRecord(a, nullptr);
         if (form == 0) hipLaunchKernelGGL(mfma_loop<0>, dim3(blocks), dim3(256), 0, nullptr, out, iters, r);
-        else hipLaunchKernelGGL(mfma_loop<1>, dim3(blocks), dim3(256), 0, nullptr, out, iters, r);
+        else if (form == 1) hipLaunchKernelGGL(mfma_loop<1>, dim3(blocks), dim3(256), 0, nullptr, out, iters, r);
+        else hipLaunchKernelGGL(mfma_loop<2>, dim3(blocks), dim3(256), 0, nullptr, out, iters, r);
         e = hipGetLastError();
         (void)hipEventRecord(b, nullptr);
         if (e == hipSuccess) e = hipEventSynchronize(b);
@@ -157,8 +177,10 @@ int sllm_probe_mfma_tops(int form, int blocks, int iters, int reps, double *tops
     (void)hipEventDestroy(b);
     (void)hipFree(out);
     if (e != hipSuccess) return (int)e;
-    const double k = form == 0 ? 32.0 : 64.0;
-    const double ops = 2.0 * 16 * 16 * k * (double)kChains * iters * blocks * 4;  // 4 waves per workgroup
+    // MACs per wave per loop trip: kChains 16 x 16 x K MFMAs (forms 0, 1) or
+    // four 32 x 32 x 32 ones (form 2)
+    const double macs = form == 0 ? 16.0 * 16 * 32 * kChains : form == 1 ? 16.0 * 16 * 64 * kChains : 32.0 * 32 * 32 * 4;
+    const double ops = 2.0 * macs * iters * blocks * 4;  // 4 waves per workgroup
     *tops = ops / (best * 1e-3) / 1e12;
     return 0;
 }
