@@ -461,7 +461,16 @@ sllm_status with_upload(const void *host, size_t bytes, size_t extra, F fn) {
 }
 
 bool uses_gemm(const sllm_weight *w, int x_rows) {
-    return x_rows >= tuning().gemm_min_rows && gemm_supported(w->fmt, w->groups);
+    // 0 (the default): the GEMM from 8 activation rows for weights of at least
+    // 2^24 elements, from 16 for smaller ones. The GEMV takes up to 4 rows per
+    // launch and streams the weight once per launch; the GEMM streams it once.
+    // Measured (us, GEMV at M = 8 / GEMM at M = 8): Q4_1 14336x4096 36.0 /
+    // 28.3, Q8_0 4096x14336 54.6 / 42.4, Q5K1 4096x4096 20.2 / 17.7; Q4_1
+    // 1024x4096 at M = 8 13.7 / 20.1 and M = 16 27.2 / 19.1, Q4_0 8192x2048 at
+    // M = 16 30.5 / 17.9.
+    int min_rows = tuning().gemm_min_rows;
+    if (min_rows == 0) min_rows = (int64_t)w->rows * w->cols >= ((int64_t)1 << 24) ? 8 : 16;
+    return x_rows >= min_rows && gemm_supported(w->fmt, w->groups);
 }
 
 // The GEMV kernel format of a weight, fixed by its plane layout at load: Q4_K
@@ -703,8 +712,9 @@ const char *sllm_kernel_info(void) {
     char buf[512];
     std::snprintf(buf, sizeof buf,
                   "sllm_qmm gfx950 planes-v1 | gemv: persistent, <=%d waves/WG, %d WG/CU, fused Q8_0 LDS "
-                  "prologue, non-temporal weight stream | gemm: int8 MFMA from xRows>=%d",
-                  t.gemv_waves, t.gemv_wg_per_cu, t.gemm_min_rows);
+                  "prologue, non-temporal weight stream | gemm: int8 MFMA from xRows>=%s",
+                  t.gemv_waves, t.gemv_wg_per_cu,
+                  t.gemm_min_rows ? std::to_string(t.gemm_min_rows).c_str() : "8 (16 below 2^24 weights)");
     info = buf;
     return info.c_str();
 }
@@ -719,8 +729,8 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "attn_tile_groups") && value >= 1 && value <= 4) t.attn_tile_groups = value;
     else if (!std::strcmp(name, "attn_head_slices") && value >= 0 && value <= 64) t.attn_head_slices = value;
-    else if (!std::strcmp(name, "gemm_shape") && value >= 0 && value <= 3) t.gemm_shape = value;
-    else if (!std::strcmp(name, "gemm_min_rows") && value >= 1) t.gemm_min_rows = value;
+    else if (!std::strcmp(name, "gemm_shape") && value >= 0 && value <= 4) t.gemm_shape = value;
+    else if (!std::strcmp(name, "gemm_min_rows") && value >= 0) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemm_splits") && value >= 0 && value <= 64) t.gemm_splits = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;
     else if (!std::strcmp(name, "gemv_q6k_stream") && (value == 0 || value == 1)) t.gemv_q6k_stream = value;

@@ -690,11 +690,15 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
 // kWide: 64 x 128 tiles, the blocks of a stage software-pipelined, one stage
 // of global loads in flight. kDeep: 64 x 64 tiles, two waves per 32 x 64
 // taking alternate blocks of each stage, pipelined. kDeepS: kDeep computing
-// one block at a time, two stages of global loads in flight.
-enum GemmShape { kWide = 0, kDeep = 1, kDeepS = 2 };
+// one block at a time, two stages of global loads in flight. kDeepS32: 32 x 64
+// tiles whose 4 waves take one block of each 4-block stage each (one block at
+// a time, two stages in flight), for Q5K1 with up to 32 activation rows (the
+// other formats measure faster on 64-row tiles even then: Q8_0 4096x14336 at
+// M = 32 on 32 x 256 tiles 46.8 us against 34.7 at M = 33 on kWide).
+enum GemmShape { kWide = 0, kDeep = 1, kDeepS = 2, kDeepS32 = 3 };
 
 struct GemmPlan {
-    int shape, bn, kb, splits, sps, mtiles, ntiles;
+    int shape, bm, bn, kb, splits, sps, mtiles, ntiles;
 };
 
 GemmPlan plan_gemm_q5(int M, int N, int G) {
@@ -710,8 +714,8 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
     return p;
 }
 
-constexpr int kGemmBM = 64;
-constexpr int shape_bn(int fmt, int shape) { return shape == kWide ? 128 : 64; }
+constexpr int shape_bm(int shape) { return shape == kDeepS32 ? 32 : 64; }
+constexpr int shape_bn(int shape) { return shape == kWide ? 128 : 64; }
 constexpr int shape_kb(int shape) { return 4; }
 
 GemmPlan plan_gemm(int fmt, int M, int N, int G) {
@@ -724,11 +728,14 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     // deep 41 / 62 / 212; Q8_0 4096x14336 wide 37 / 52 / 148, deep 39 / 59 /
     // 180; Q5K1 14336x4096 kDeepS 52 / 85 / 276, kDeep 54 / 84 / 306, wide
     // 100 / 168 / 575 (its wide tiles spill).
-    p.shape = fmt == SLLM_Q5K1 ? kDeepS : kWide;
-    if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 3) p.shape = tuning().gemm_shape - 1;
-    p.bn = shape_bn(fmt, p.shape);
+    // (Q5K1 with up to 32 activation rows: 32-row tiles; Q5K1 4096x4096 at M
+    // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.)
+    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : kWide;
+    if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 4) p.shape = tuning().gemm_shape - 1;
+    p.bm = shape_bm(p.shape);
+    p.bn = shape_bn(p.shape);
     p.kb = shape_kb(p.shape);
-    p.mtiles = (M + kGemmBM - 1) / kGemmBM;
+    p.mtiles = (M + p.bm - 1) / p.bm;
     p.ntiles = (N + p.bn - 1) / p.bn;
     const int nst = G / p.kb;
     // K splits double until there are 1.5 workgroups per CU, each split keeping >= 2 stages
@@ -761,6 +768,7 @@ sllm_status launch_fmt(const Planes &P, const int8_t *xq, const float *xsp, cons
     switch (p.shape) {
     case kDeep: return launch_shape<FMT, 2, 1, 2, 2, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     case kDeepS: return launch_shape<FMT, 2, 1, 2, 2, 4, false, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case kDeepS32: return launch_shape<FMT, 1, 1, 2, 4, 4, false, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     default: return launch_shape<FMT, 2, 2, 2, 1, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     }
 }

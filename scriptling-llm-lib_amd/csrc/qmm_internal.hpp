@@ -258,7 +258,7 @@ struct Tuning {
     int gemv_wg_per_cu = 1;    // GEMV workgroups per CU (persistent grid = CUs x this)
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
-    int gemm_min_rows = 64;    // xRows at which the MFMA GEMM takes over
+    int gemm_min_rows = 0;     // xRows at which the MFMA GEMM takes over (0: 8, or 16 below 2^24 weights)
     int gemm_shape = 0;        // GEMM workgroup shape (1..3; 0: by format)
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // load option: Q4_K weights keep (and stream) the GGUF headers (1) or not (0, faster)

@@ -29,7 +29,7 @@ def slice_rows(qtype: str, raw: np.ndarray, N: int, G: int, rows: np.ndarray) ->
 
 
 @pytest.mark.parametrize("qtype", QTYPES)
-@pytest.mark.parametrize("M", [64, 65, 130])
+@pytest.mark.parametrize("M", [8, 17, 33, 64, 65, 130])
 @pytest.mark.parametrize("N,K", [(96, 512), (200, 1024)])
 def test_prefill_parity(qtype, M, N, K):
     if qtype == "q5k1" and K % 256:
@@ -43,7 +43,8 @@ def test_prefill_parity(qtype, M, N, K):
 
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
-@pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1), (3, 1), (3, 3), (3, 8)])
+@pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1), (3, 1), (3, 3), (3, 8),
+                                          (4, 1), (4, 3)])
 def test_shape_and_split_overrides(qtype, shape, splits):
     # every workgroup shape and any K split count gives the oracle's result
     # within the bound (K = 1024 is 8 stages: 5 splits of 2 stages leave the
@@ -81,7 +82,7 @@ def _block_dots_case(qtype, raw, N, K, x, row0, n_rows, shape=0):
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
 @pytest.mark.parametrize("M", [64, 130])
-@pytest.mark.parametrize("shape", [1, 2, 3])
+@pytest.mark.parametrize("shape", [1, 2, 3, 4])
 def test_gemm_block_dots_bitexact(qtype, M, shape):
     # the int32 block dots the matrix cores return, read from the registers the
     # epilogue scales, against the oracle's per-(row, block) dots
