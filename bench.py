@@ -35,7 +35,7 @@ sys.path.insert(0, os.path.join(ROOT, "scriptling-llm-lib_amd"))
 
 HBM_PEAK_GBS = 8000.0
 INT8_MFMA_PEAK_TOPS = 5000.0
-VALU_PEAK_TOPS = 78.6  # fp32 VALU lane-ops/s in T: 157.3 TFLOP/s vector peak counts an FMA as 2; mul and add issue at the same lane rate
+BF16_MFMA_PEAK_TOPS = 2500.0  # MI355X dense bf16 matrix peak (TFLOP/s)
 METRIC = "quant GEMV GB/s (% of 8 TB/s HBM); Q4_K_M 8B-shape decode tok/s"
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_gemv_q4_1_gate_up_c3.json")
 ROTATE_BYTES = 1 << 30  # weight copies per timed kernel: > 4x the 256 MB MALL
@@ -288,9 +288,10 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
     Each entry rotates over copies of its weight totalling >= 1 GiB (at most
     512 copies, so C1's 0.9 MB weight can stay in the MALL: C1 is launch-bound
     at any rate). GEMV lines give GB/s of algorithmic bytes; GEMM lines (M >=
-    64) also give TOPS (2 M N K per call) against the published 5.0 POPS dense
-    int8 MFMA peak, or for Q5_0 (fp32 activations, exact per-block sums on the VALU at 2
-    ops per MAC) against the 78.6 T lane-ops/s VALU peak. Q5_K rows stream 26 B / 32 weights (the two Q4_1 halves of
+    8 or 16) also give TOPS (2 M N K per call) against the published 5.0 POPS
+    dense int8 MFMA peak, or for Q5_0 (fp32 activations split into three exact
+    bf16 parts, so the bf16 matrix cores execute 3 x 2 M N K) against the 2.5
+    PFLOP/s dense bf16 peak. Q5_K rows stream 26 B / 32 weights (the two Q4_1 halves of
     convertQ5KToTwoQ41 without the high half's zero mins and 4-bit codes).
     M = 1 lines also give us_graph: the per-launch time of 100 of the same
     calls replayed from one HIP graph (C1-sized GEMVs are launch-bound)."""
@@ -329,9 +330,9 @@ def config_table(sq, synth, torch, stream, peaks=None) -> dict:
         if M >= 64:
             tops = 2.0 * M * N * K / (us * 1e-6) / 1e12
             if ws[0].qtype == "q5":
-                # fp32 activations: exact per-block sums on the VALU, 2 ops per MAC
-                r.update({"TOPS": round(tops, 1), "frac_valu": round(tops / VALU_PEAK_TOPS, 4),
-                          "path": "VALU GEMM (Q5_0 keeps fp32 activations)"})
+                # fp32 activations as three exact bf16 parts: 3 x 2 M N K on the bf16 matrix cores
+                r.update({"TOPS": round(tops, 1), "frac_bf16_mfma": round(3 * tops / BF16_MFMA_PEAK_TOPS, 4),
+                          "path": "bf16 MFMA GEMM (Q5_0 keeps fp32 activations, split into three bf16 parts)"})
             else:
                 r.update({"TOPS": round(tops, 1), "frac_int8_mfma": round(tops / INT8_MFMA_PEAK_TOPS, 4),
                           "path": "int8 MFMA GEMM"})

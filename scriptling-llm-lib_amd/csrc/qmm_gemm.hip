@@ -1,5 +1,6 @@
-// Prefill GEMM (xRows >= 64): int8 matrix cores for Q8_0 / Q4_0 / Q4_1 / Q5K1,
-// and a VALU GEMM for Q5_0 (fp32 activations; see gemm_q5_kernel below).
+// Prefill GEMM (xRows >= 8 or 16): int8 matrix cores for Q8_0 / Q4_0 / Q4_1 /
+// Q5K1, and bf16 matrix cores for Q5_0 (fp32 activations split exactly into
+// three bf16 parts; see gemm_q5_kernel below).
 //
 // 1. The activation rows are quantized once into a workspace (xq int8 [M][K],
 //    xs fp32 [M][G], Σxq int32 [M][G]) by the GEMV prologue's routine.
@@ -518,84 +519,194 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
 
 // ------------------------------------------------------------- Q5_0 ----
 //
-// Q5_0 keeps fp32 activations (no int8 operand, float32_ops.go:427-436), so
-// its prefill GEMM runs on the VALU. Each output's per-block sum is formed in
-// the reference's operation order (q5DotGroupXF32, float32_ops.go:335-367):
-// for j = 0..15, p0 = v0*x[j], p1 = v1*x[j+16], sum = sum + (p0 + p1), with
-// v = float(q5) - 16; then term = d * sum, accumulated block by block. That
-// is two fp32 VALU ops per weight and activation, so the VALU bounds it.
-// A workgroup of 256 threads owns a 64 x 64 tile of dst; thread (tm, tn)
-// owns activation rows tm + 16 r and weight rows tn + 16 c (r, c < 4). Per
-// block the x tile and the decoded weight tile (fp32) are staged in LDS,
-// double-buffered: the next block's global loads are in flight during the
-// current block's arithmetic.
-constexpr int kQ5Tile = 64;
-constexpr int kQ5Stride = 36;  // floats per LDS row: 16-byte aligned, rows spread over the banks
+// Q5_0 keeps fp32 activations (no int8 operand, float32_ops.go:427-436): each
+// block's sum is sum_j v_j x_j over its 32 elements (v = q5 - 16, the pairs j
+// and j + 16 added in j order by q5DotGroupXF32, float32_ops.go:335-367), then
+// term = d * sum. On the matrix cores:
+// * a pre-pass splits every activation exactly into three bf16 parts, x = hi
+//   + mid + lo: hi the top 8 significand bits (truncated), mid the next 8 of
+//   the remainder, lo the remainder itself, which has at most 8 significant
+//   bits left and so is a bf16 (a non-finite x: hi = x, mid = lo = 0);
+// * v is a small integer, exact in bf16, so v_mfma_f32_32x32x16_bf16 over the
+//   three parts forms every product v * part exactly and each block's sum in
+//   fp32 (summed in the matrix core's order instead of the reference's j
+//   order: reassociation only);
+// * the epilogue adds the block term with one fused multiply-add,
+//   acc = fma(f16lut(d), sum, acc) (the reference rounds d * sum first).
+// A workgroup of 4 waves owns a 64 x 128 tile (each wave 32 x 64: two 32 x 32
+// MFMA tiles); one block per K stage through LDS, double-buffered; split-K
+// with the fixed-order reduction when tiles are few.
 
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+constexpr int kQ5BM = 64;
+constexpr int kQ5Pieces = kQ5BM * 12;  // 16-byte pieces of a block-stage's activation parts
+constexpr int kQ5Row = 40;  // bf16 per LDS row of one block: 32 + 8 pad (80 B: conflict-free b128 reads)
+
+// x [M][K] fp32 -> xs3 [M][G][3][32] bf16: the hi, mid and lo parts of each block.
+__global__ void split_act_kernel(const float *__restrict__ x, size_t nblocks, uint16_t *__restrict__ xs3) {
+    // one thread per 8 elements (two float4)
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nblocks * 4;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const size_t blk = i >> 2;
+        const int c = (int)(i & 3);
+        const float4 *src = (const float4 *)(x + blk * 32 + 8 * c);
+        const float4 u0 = src[0], u1 = src[1];
+        const float v[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+        uint32_t hi[4], mid[4], lo[4];
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            uint32_t ph[2], pm[2], pl[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const float f = v[k + e];
+                const uint32_t ub = __float_as_uint(f);
+                if ((ub & 0x7f800000u) == 0x7f800000u) {  // Inf / NaN: the value itself, no remainder
+                    ph[e] = ub >> 16;
+                    pm[e] = pl[e] = 0;
+                    continue;
+                }
+                const float h = __uint_as_float(ub & 0xffff0000u);
+                const float r1 = f - h;  // exact
+                const float m = __uint_as_float(__float_as_uint(r1) & 0xffff0000u);
+                const float r2 = r1 - m;  // exact, and a bf16
+                ph[e] = ub >> 16;
+                pm[e] = __float_as_uint(m) >> 16;
+                pl[e] = __float_as_uint(r2) >> 16;
+            }
+            hi[k >> 1] = ph[0] | (ph[1] << 16);
+            mid[k >> 1] = pm[0] | (pm[1] << 16);
+            lo[k >> 1] = pl[0] | (pl[1] << 16);
+        }
+        uint16_t *dst = xs3 + blk * 96 + 8 * c;
+        *(uint4 *)dst = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        *(uint4 *)(dst + 32) = make_uint4(mid[0], mid[1], mid[2], mid[3]);
+        *(uint4 *)(dst + 64) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    }
+}
+
+template <int BN>
 struct alignas(16) Q5Stage {
-    float x[kQ5Tile * kQ5Stride];
-    float v[kQ5Tile * kQ5Stride];
-    float d[kQ5Tile];
+    uint16_t a[3][kQ5BM][kQ5Row];  // activation parts (bf16), elements in block order
+    uint16_t b[BN][kQ5Row];        // weights q5 - 16 (bf16, exact)
+    float d[BN];                   // f16lut(d) (the reference's table decode)
 };
 
-// This thread's share of one block's global operands: two float4 of x (rows
-// t/8 and t/8 + 32) and four nibble bytes + high bits + scale of weight row t/4.
-typedef float v4f __attribute__((ext_vector_type(4)));
-
+// One thread's share of one block-stage (T = 2 BN threads): pieces t, t + T,
+// ... of the activation parts (64 rows x 3 parts x 4 pieces of 16 bytes), and
+// half a weight row's block (row t / 2, elements 8 h .. 8 h + 7 and their + 16
+// partners, h = t % 2).
+template <int T>
 struct Q5Fetch {
-    v4f x0, x1;
-    uint32_t qs, qh;
+    static constexpr int A_PER = (kQ5Pieces + T - 1) / T;
+    int4 a[A_PER];
+    uint2 qs;
+    uint32_t qh;
     uint16_t d;
 };
 
-__device__ __forceinline__ void q5_fetch(const Planes &P, const float *__restrict__ x, int M, int N, int G, int m0,
-                                         int n0, int g, Q5Fetch &f) {
+template <int T>
+__device__ __forceinline__ void q5m_fetch(Q5Fetch<T> &f, const Planes &P, const uint16_t *__restrict__ xs3, int M,
+                                          int N, int G, int m0, int n0, int g) {
     const int t = threadIdx.x;
-    // rows past M / N load the last row again; their outputs are not stored
-    const int r = t >> 3, c = t & 7;
-    const int ma = min(m0 + r, M - 1), mb = min(m0 + r + 32, M - 1);
-    f.x0 = *((const v4f *)(x + ((size_t)ma * G + g) * 32) + c);
-    f.x1 = *((const v4f *)(x + ((size_t)mb * G + g) * 32) + c);
-    const int n = min(n0 + (t >> 2), N - 1);
+#pragma unroll
+    for (int i = 0; i < Q5Fetch<T>::A_PER; i++) {
+        const int e = t + T * i;  // piece e: row e / 12, part (e % 12) / 4, 16 bytes e % 4
+        if (kQ5Pieces % T == 0 || e < kQ5Pieces) {
+            const int m = min(m0 + e / 12, M - 1);  // rows past M reload the last row; never stored
+            const int rem = e % 12;
+            f.a[i] = *(const int4 *)(xs3 + ((size_t)m * G + g) * 96 + (rem >> 2) * 32 + (rem & 3) * 8);
+        }
+    }
+    const int n = min(n0 + (t >> 1), N - 1);
     const size_t idx = (size_t)n * G + g;
-    f.qs = ((const uint32_t *)(P.qs + idx))[t & 3];
+    f.qs = ((const uint2 *)(P.qs + idx))[t & 1];
     f.qh = P.qh[idx];
     f.d = P.d[idx];
 }
 
-__device__ __forceinline__ void q5_store(Q5Stage &S, const Q5Fetch &f) {
+// bf16 bits of the small integer v (exact).
+__device__ __forceinline__ uint32_t bf16_of_int(int v) { return __float_as_uint((float)v) >> 16; }
+
+template <int T>
+__device__ __forceinline__ void q5m_store(const Q5Fetch<T> &f, Q5Stage<T / 2> &S) {
     const int t = threadIdx.x;
-    const int r = t >> 3, c = t & 7;
-    *(v4f *)(S.x + r * kQ5Stride + 4 * c) = f.x0;
-    *(v4f *)(S.x + (r + 32) * kQ5Stride + 4 * c) = f.x1;
-    // weight row t/4, elements 4 part .. 4 part + 3 (low nibbles) and 16 + those
-    // (high nibbles); bit e of qh is bit 4 of element e (gguf.go:472-490)
-    const int row = t >> 2, part = t & 3;
-    float lo[4], hi[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int e = 4 * part + i;
-        const uint32_t b = (f.qs >> (8 * i)) & 0xffu;
-        const int q0 = (int)((b & 0x0fu) | (((f.qh >> e) & 1u) << 4));
-        const int q1 = (int)((b >> 4) | (((f.qh >> (e + 16)) & 1u) << 4));
-        lo[i] = (float)q0 - 16.0f;
-        hi[i] = (float)q1 - 16.0f;
+    for (int i = 0; i < Q5Fetch<T>::A_PER; i++) {
+        const int e = t + T * i;
+        if (kQ5Pieces % T == 0 || e < kQ5Pieces) {
+            const int rem = e % 12;
+            *(int4 *)&S.a[rem >> 2][e / 12][(rem & 3) * 8] = f.a[i];
+        }
     }
-    *(v4f *)(S.v + row * kQ5Stride + 4 * part) = v4f{lo[0], lo[1], lo[2], lo[3]};
-    *(v4f *)(S.v + row * kQ5Stride + 16 + 4 * part) = v4f{hi[0], hi[1], hi[2], hi[3]};
-    if (part == 0) S.d[row] = f16_lut(f.d);
+    // weight row t / 2: nibble bytes 8 h .. 8 h + 7 hold elements j (low) and
+    // j + 16 (high); bit e of qh is bit 4 of element e (gguf.go:472-490)
+    const int row = t >> 1, h = t & 1;
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+        uint32_t pl[2], ph[2];
+#pragma unroll
+        for (int e2 = 0; e2 < 2; e2++) {
+            const int k2 = k + e2;
+            const uint32_t byte = ((k2 < 4 ? f.qs.x : f.qs.y) >> (8 * (k2 & 3))) & 0xffu;
+            const int j = 8 * h + k2;
+            const int q0 = (int)((byte & 0x0fu) | (((f.qh >> j) & 1u) << 4));
+            const int q1 = (int)((byte >> 4) | (((f.qh >> (j + 16)) & 1u) << 4));
+            pl[e2] = bf16_of_int(q0 - 16);
+            ph[e2] = bf16_of_int(q1 - 16);
+        }
+        lo[k >> 1] = pl[0] | (pl[1] << 16);
+        hi[k >> 1] = ph[0] | (ph[1] << 16);
+    }
+    *(uint4 *)&S.b[row][8 * h] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *(uint4 *)&S.b[row][16 + 8 * h] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+    if (h == 0) S.d[row] = f16_lut(f.d);
 }
 
-__device__ __forceinline__ float comp(const v4f &v, int k) { return v[k]; }
+// One block's MFMAs and epilogue for one wave's 32 x 64 tile.
+template <int BN>
+__device__ __forceinline__ void q5m_block(const Q5Stage<BN> &S, int wm, int wn, int r32, int h, float (&acc)[2][16]) {
+    // operands: step s covers elements 16 s .. 16 s + 15, lane half h 8 of them
+    v8bf a[3][2], b[2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++) {
+#pragma unroll
+        for (int part = 0; part < 3; part++)
+            a[part][s2] = __builtin_bit_cast(v8bf, *(const int4 *)&S.a[part][wm * 32 + r32][16 * s2 + 8 * h]);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            b[j][s2] = __builtin_bit_cast(v8bf, *(const int4 *)&S.b[wn * 64 + 32 * j + r32][16 * s2 + 8 * h]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        v16f sum = {};
+#pragma unroll
+        for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+            for (int part = 0; part < 3; part++)
+                sum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[part][s2], b[j][s2], sum, 0, 0, 0);
+        const float dd = S.d[wn * 64 + 32 * j + r32];
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[j][v] = __builtin_fmaf(dd, sum[v], acc[j][v]);
+    }
+}
 
-// Tile (mt, nt) of split sp; blocks [sp * bps, min(G, (sp + 1) * bps)).
-__global__ void __launch_bounds__(256, 4) gemm_q5_kernel(Planes P, const float *__restrict__ x,
+// Tile (mt, nt) of split sp; blocks [sp * bps, min(G, (sp + 1) * bps)); a
+// workgroup of 2 x WN waves owns a 64 x 64 WN tile. PF: blocks of global loads
+// in flight (two register sets filled alternately).
+template <int WN, int PF>
+__global__ void __launch_bounds__(128 * WN) gemm_q5_kernel(Planes P, const uint16_t *__restrict__ xs3,
                                                       float *__restrict__ out, int M, int N, int G, int mtiles,
                                                       int ntiles, int splits, int bps) {
+    constexpr int BN = 64 * WN, T = 128 * WN;
     extern __shared__ __attribute__((aligned(16))) unsigned char lds_raw[];
-    Q5Stage *st = (Q5Stage *)lds_raw;
+    Q5Stage<BN> *st = (Q5Stage<BN> *)lds_raw;
     // XCD-aware order, as in gemm_kernel: the M-tiles of one weight tile and
-    // split run on one XCD, so the weight tile is read from HBM once into its L2
+    // split run on one XCD, so the weight tile is read from HBM once into its
+    // L2 (measured against the other way round, one activation tile per XCD:
+    // 14336x4096 at M = 512 648 against 853 us)
     const int total = mtiles * ntiles * splits;
     const int per_xcd = (total + 7) / 8;
     const int lin = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
@@ -603,76 +714,63 @@ __global__ void __launch_bounds__(256, 4) gemm_q5_kernel(Planes P, const float *
     const int mt = lin % mtiles;
     const int rest = lin / mtiles;
     const int sp = rest % splits, nt = rest / splits;
-    const int m0 = mt * kQ5Tile, n0 = nt * kQ5Tile;
+    const int m0 = mt * kQ5BM, n0 = nt * BN;
     const int g0 = sp * bps, g1 = min(G, g0 + bps);
-    const int tn = threadIdx.x & 15, tm = threadIdx.x >> 4;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int r32 = lane & 31, h = lane >> 5;
 
-    float acc[4][4], sum[4][4];
+    float acc[2][16];
 #pragma unroll
-    for (int r = 0; r < 4; r++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc[r][c] = 0.0f;
+        for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
 
-    Q5Fetch f;
-    if (g0 < g1) {
-        q5_fetch(P, x, M, N, G, m0, n0, g0, f);
-        q5_store(st[0], f);
-    }
-    __syncthreads();
-    for (int g = g0; g < g1; g++) {
-        const int cur = (g - g0) & 1;
-        if (g + 1 < g1) q5_fetch(P, x, M, N, G, m0, n0, g + 1, f);
-        const Q5Stage &S = st[cur];
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-#pragma unroll
-            for (int c = 0; c < 4; c++) sum[r][c] = 0.0f;
-#pragma unroll 1
-        for (int j0 = 0; j0 < 16; j0 += 4) {
-            // elements j0..j0+3 and 16+j0..: each output's sum still adds its
-            // pairs in increasing j (the order across outputs is free)
-            v4f xa[4], xb[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                xa[r] = *(const v4f *)(S.x + (tm + 16 * r) * kQ5Stride + j0);
-                xb[r] = *(const v4f *)(S.x + (tm + 16 * r) * kQ5Stride + 16 + j0);
-            }
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const v4f va = *(const v4f *)(S.v + (tn + 16 * c) * kQ5Stride + j0);
-                const v4f vb = *(const v4f *)(S.v + (tn + 16 * c) * kQ5Stride + 16 + j0);
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        const float p0 = comp(va, k) * comp(xa[r], k);
-                        const float p1 = comp(vb, k) * comp(xb[r], k);
-                        const float pair = p0 + p1;
-                        sum[r][c] = sum[r][c] + pair;
-                    }
-            }
+    if (PF == 1) {
+        Q5Fetch<T> f;
+        if (g0 < g1) {
+            q5m_fetch(f, P, xs3, M, N, G, m0, n0, g0);
+            q5m_store(f, st[0]);
         }
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const float dd = S.d[tn + 16 * c];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const float grp = dd * sum[r][c];
-                acc[r][c] = acc[r][c] + grp;
-            }
-        }
-        if (g + 1 < g1) q5_store(st[cur ^ 1], f);
         __syncthreads();
+        for (int g = g0; g < g1; g++) {
+            const int cur = (g - g0) & 1;
+            if (g + 1 < g1) q5m_fetch(f, P, xs3, M, N, G, m0, n0, g + 1);
+            q5m_block(st[cur], wm, wn, r32, h, acc);
+            if (g + 1 < g1) q5m_store(f, st[cur ^ 1]);
+            __syncthreads();
+        }
+    } else {
+        Q5Fetch<T> fa, fb;
+        if (g0 < g1) {
+            q5m_fetch(fa, P, xs3, M, N, G, m0, n0, g0);
+            if (g0 + 1 < g1) q5m_fetch(fb, P, xs3, M, N, G, m0, n0, g0 + 1);
+            q5m_store(fa, st[0]);
+        }
+        __syncthreads();
+        for (int g = g0; g < g1; g += 2) {
+            // block g: fb holds block g + 1
+            if (g + 2 < g1) q5m_fetch(fa, P, xs3, M, N, G, m0, n0, g + 2);
+            q5m_block(st[(g - g0) & 1], wm, wn, r32, h, acc);
+            if (g + 1 < g1) q5m_store(fb, st[(g + 1 - g0) & 1]);
+            __syncthreads();
+            if (g + 1 >= g1) break;
+            // block g + 1: fa holds block g + 2
+            if (g + 3 < g1) q5m_fetch(fb, P, xs3, M, N, G, m0, n0, g + 3);
+            q5m_block(st[(g + 1 - g0) & 1], wm, wn, r32, h, acc);
+            if (g + 2 < g1) q5m_store(fa, st[(g + 2 - g0) & 1]);
+            __syncthreads();
+        }
     }
 
     float *o = out + (size_t)sp * M * N;  // splits > 1: partial tile of split sp
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int m = m0 + tm + 16 * r;
+    for (int j = 0; j < 2; j++) {
+        const int n = n0 + wn * 64 + 32 * j + r32;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int n = n0 + tn + 16 * c;
-            if (m < M && n < N) o[(size_t)m * N + n] = acc[r][c];
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + wm * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            if (m < M && n < N) o[(size_t)m * N + n] = acc[j][v];
         }
     }
 }
@@ -705,10 +803,22 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
     const int cus = 256;
     GemmPlan p{};
     p.shape = 0;
-    p.mtiles = (M + kQ5Tile - 1) / kQ5Tile;
-    p.ntiles = (N + kQ5Tile - 1) / kQ5Tile;
+    p.bm = kQ5BM;
+    // 64 x 256 tiles (8 waves) halve the activation parts' re-reads across
+    // N-tiles: 14336x4096 at M = 16 / 64 / 128 / 512 82.6 / 93.9 / 155.1 /
+    // 456.5 us against 95.7 / 107.2 / 183.3 / 644.7 on 64 x 128 tiles (4
+    // waves), which stay ahead for narrow weights at few rows (1024x4096 at
+    // M = 16 / 64 / 128: 24.1 / 27.3 / 32.1 against 27.2 / 29.7 / 34.4)
+    p.bn = (N >= 4096 || M > 128) ? 256 : 128;
+    if (tuning().gemm_shape == 1) p.bn = 256;
+    if (tuning().gemm_shape == 2) p.bn = 128;
+    p.kb = 1;
+    p.mtiles = (M + kQ5BM - 1) / kQ5BM;
+    p.ntiles = (N + p.bn - 1) / p.bn;
+    // K splits double until there are 1.5 workgroups per CU, each split keeping >= 4 blocks
     int S = 1;
-    while ((int64_t)p.mtiles * p.ntiles * S < 2 * cus && G / (S * 2) >= 4) S *= 2;
+    while ((int64_t)p.mtiles * p.ntiles * S * 2 < 3 * cus && G / (S * 2) >= 4) S *= 2;
+    if (tuning().gemm_splits) S = tuning().gemm_splits < G ? tuning().gemm_splits : G;
     p.splits = S;
     p.sps = (G + S - 1) / S;  // blocks per split
     return p;
@@ -796,10 +906,22 @@ sllm_status gemm_impl(int fmt, const Planes &P, const float *x, float *dst, int 
     float *part;
     if (fmt == SLLM_Q5_0) {
         if (dots) return set_error(SLLM_ERR_QTYPE, "gemm block dots: Q5_0 has no int8 GEMM");
-        part = (float *)ws;
+        uint16_t *xs3 = (uint16_t *)ws;
+        part = (float *)((char *)ws + align256((size_t)M * G * 96 * sizeof(uint16_t)));
+        const size_t nblocks = (size_t)M * G;
+        int sgrid = (int)((nblocks * 4 + 255) / 256);
+        if (sgrid > 4096) sgrid = 4096;
+        hipLaunchKernelGGL(split_act_kernel, dim3(sgrid), dim3(256), 0, s, x, nblocks, xs3);
+        SLLM_HIP(hipGetLastError());
         const int total = p.mtiles * p.ntiles * p.splits;
-        hipLaunchKernelGGL(gemm_q5_kernel, dim3(((total + 7) / 8) * 8), dim3(256), 2 * sizeof(Q5Stage), s, P, x,
-                           p.splits > 1 ? part : dst, M, N, G, p.mtiles, p.ntiles, p.splits, p.sps);
+        dim3 grid(((total + 7) / 8) * 8);
+        float *o = p.splits > 1 ? part : dst;
+        if (p.bn == 256)
+            hipLaunchKernelGGL((gemm_q5_kernel<4, 1>), grid, dim3(512), 2 * sizeof(Q5Stage<256>), s, P, xs3, o, M, N,
+                               G, p.mtiles, p.ntiles, p.splits, p.sps);
+        else
+            hipLaunchKernelGGL((gemm_q5_kernel<2, 1>), grid, dim3(256), 2 * sizeof(Q5Stage<128>), s, P, xs3, o, M, N,
+                               G, p.mtiles, p.ntiles, p.splits, p.sps);
         SLLM_HIP(hipGetLastError());
     } else {
         int8_t *xq = (int8_t *)ws;
@@ -832,7 +954,7 @@ bool gemm_supported(int fmt, int G) {
 size_t gemm_workspace_bytes(int fmt, int N, int G, int M) {
     const GemmPlan p = plan_gemm(fmt, M, N, G);
     const size_t parts = p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
-    if (fmt == SLLM_Q5_0) return align256(parts);
+    if (fmt == SLLM_Q5_0) return align256((size_t)M * G * 96 * sizeof(uint16_t)) + align256(parts);
     return align256((size_t)M * G * 32) + 2 * align256((size_t)M * G * 4) + align256(parts);
 }
 
