@@ -421,11 +421,13 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
  *                                  weights of 2^24 elements or more, 16 for smaller ones;
  *                                  the GEMM and GEMV sum a row's blocks in different
  *                                  orders, so a row's last bits can change with it)
- *   gemm_shape          0..4       GEMM workgroups: 1 = 64 x 128 tiles, 2 = 64 x 64 tiles with
+ *   gemm_shape          0..5       GEMM workgroups: 1 = 64 x 128 tiles, 2 = 64 x 64 tiles with
  *                                  each K stage split over two waves, 3 = as 2 with two
  *                                  stages of loads in flight, 4 = 32 x 64 tiles with each
- *                                  stage split over four waves (0: 1, or for Q5K1 3, and 4
- *                                  up to 32 rows; the shape moves the fp32 summation splits)
+ *                                  stage split over four waves, 5 = as 1 with two stages of
+ *                                  loads in flight (0: 1 up to 128 rows and 5 above, or for
+ *                                  Q5K1 3, and 4 up to 32 rows; the shape moves the fp32
+ *                                  summation splits)
  *   gemm_splits         0..64      GEMM K splits, added in split order (0: by tile count;
  *                                  the split count moves the fp32 summation splits)
  *   attn_target_blocks  1..65536   attention: about this many workgroups when splitting (512)

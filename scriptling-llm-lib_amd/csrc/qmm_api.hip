@@ -729,7 +729,7 @@ sllm_status sllm_set_param(const char *name, int value) {
     else if (!std::strcmp(name, "attn_target_blocks") && value >= 1 && value <= 65536) t.attn_target_blocks = value;
     else if (!std::strcmp(name, "attn_tile_groups") && value >= 1 && value <= 4) t.attn_tile_groups = value;
     else if (!std::strcmp(name, "attn_head_slices") && value >= 0 && value <= 64) t.attn_head_slices = value;
-    else if (!std::strcmp(name, "gemm_shape") && value >= 0 && value <= 4) t.gemm_shape = value;
+    else if (!std::strcmp(name, "gemm_shape") && value >= 0 && value <= 5) t.gemm_shape = value;
     else if (!std::strcmp(name, "gemm_min_rows") && value >= 0) t.gemm_min_rows = value;
     else if (!std::strcmp(name, "gemm_splits") && value >= 0 && value <= 64) t.gemm_splits = value;
     else if (!std::strcmp(name, "gemv_q4k_stream") && (value == 0 || value == 1)) t.gemv_q4k_stream = value;

@@ -21,13 +21,19 @@
 //    kernels (q4q8_row_arm64.s, q41q8_row_arm64.s:59-63: per-lane FMLA
 //    accumulators added at the end):
 //      t   = fma(F, d, -1.5 * 2^23 * d)   = round(dot * d)  (exact addend)
-//      Q4_1 / Q5K1: t = fma(float(Σxq), m, t)              (min term)
 //      Q5K1: t = t + round(dot_high * d_high)               (high block)
 //      acc = fma(t, xs, acc)
-//    Each per-block term is rounded at most twice fewer times than in the
-//    reference's x86 order (cmb = d * xs, term = cmb * float(dot), acc += term),
-//    so every output differs from the reference's sequential sum by a few
-//    ulp of sum |term| at most; the tests hold it to 1e-5 * sum |term|.
+//    The min term of Q4_1 / Q5K1, float(Σxq) * m * xs per block, factors into
+//    a plain product over blocks, sum_g (float(Σxq) * xs)[m][g] * m[n][g]:
+//    v_mfma_f32_32x32x2_f32 adds it two blocks at a time into the same
+//    accumulator (min_piece), so the per-block VALU
+//    work is two multiply-adds for Q4_1 (three in the reference's order).
+//    Each part of a per-block term is rounded about as often as in the
+//    reference's own order (cmb = d * xs, term = cmb * float(dot), acc +=
+//    term; Q4_1: (dot * d + Σxq * m) * xs), so every output differs from the
+//    reference's sequential sum by a few ulp of sum |term| at most (|term|
+//    here counting the dot and min parts apart); the tests hold it to 1e-5 *
+//    sum |term|.
 //    A K stage whose weight scales are not finite, or whose activation scales
 //    reach 2^90 (where d * xs could overflow while dot * d does not), is
 //    computed in the reference's exact operation order instead: the choice is
@@ -53,6 +59,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kMagicBits = 0x4B400000;  // 1.5 * 2^23
 constexpr float kMagic = 12582912.0f;
@@ -218,7 +225,9 @@ struct Ops {
     float wd[CF], wm[HAS_MIN ? CF : 1], wdh[DUAL ? CF : 1];
 };
 
-template <int FMT, int KB, int BM, int BN, int CF>
+// AV: also the rows' float(Σxq) (only the exact epilogue adds the min term
+// per block; the fast path adds it on the fp32 matrix cores, see min_piece).
+template <int FMT, int KB, int BM, int BN, int CF, bool AV = false>
 __device__ __forceinline__ void load_ops(Ops<FMT, CF> &o, const Stage<FMT, KB, BM, BN> &S, int blk, int wm, int wn,
                                          int lane) {
     constexpr int RB = row_bytes(KB);
@@ -238,7 +247,7 @@ __device__ __forceinline__ void load_ops(Ops<FMT, CF> &o, const Stage<FMT, KB, B
     for (int q = 0; q < 4; q++) {
         const float4 t = *(const float4 *)&S.xs[blk][wm * 32 + 8 * q + 4 * h];
         o.xv[4 * q] = t.x; o.xv[4 * q + 1] = t.y; o.xv[4 * q + 2] = t.z; o.xv[4 * q + 3] = t.w;
-        if (O::HAS_MIN) {
+        if (O::HAS_MIN && AV) {
             const int4 u = *(const int4 *)&S.aux[O::HAS_MIN ? blk : 0][wm * 32 + 8 * q + 4 * h];
             o.av[O::HAS_MIN ? 4 * q : 0] = u.x;
             o.av[O::HAS_MIN ? 4 * q + 1 : 0] = u.y;
@@ -246,6 +255,38 @@ __device__ __forceinline__ void load_ops(Ops<FMT, CF> &o, const Stage<FMT, KB, B
             o.av[O::HAS_MIN ? 4 * q + 3 : 0] = u.w;
         }
     }
+}
+
+// The min term of Q4_1 / Q5K1 on the fp32 matrix cores: sum over blocks g of
+// float(Σxq[m][g]) * xs[m][g] * m[n][g] is a plain product of an M x G and a
+// G x N matrix, so v_mfma_f32_32x32x2_f32 adds it two blocks at a time into
+// the tile's accumulator (A: row m's fl(float(Σxq) * xs) in lane m % 32, of
+// block blkA in lanes 0..31 and blkB in lanes 32..63; B: the mins of the same
+// blocks for column n), and the per-block epilogue keeps one multiply-add
+// fewer. blkB < 0: the upper k slot is zero.
+template <int CF>
+struct MinOps {
+    float a;
+    float b[CF];
+};
+
+template <int FMT, int KB, int BM, int BN, int CF>
+__device__ __forceinline__ void load_min(MinOps<CF> &o, const Stage<FMT, KB, BM, BN> &S, int blkA, int blkB, int wm,
+                                         int wn, int lane) {
+    constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int blk = h ? blkB : blkA;
+    const bool live = blk >= 0;
+    const int bi = HAS_MIN && live ? blk : 0;
+    const int row = wm * 32 + r32;
+    o.a = live ? __int_as_float(S.aux[HAS_MIN ? bi : 0][row]) * S.xs[bi][row] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CF; j++) o.b[j] = live ? S.m[HAS_MIN ? bi : 0][wn * 32 * CF + 32 * j + r32] : 0.0f;
+}
+
+template <int CF>
+__device__ __forceinline__ void min_piece(const MinOps<CF> &o, int j, v16f &acc) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.a, o.b[j], acc, 0, 0, 0);
 }
 
 // MFMA of column piece j: D = the bits of 1.5 * 2^23 + each block dot.
@@ -258,7 +299,7 @@ __device__ __forceinline__ void mfma_piece(const Ops<FMT, CF> &o, int j, const v
 // Epilogue of column piece j: SLOW is the reference's exact operation order.
 template <int FMT, int CF, bool SLOW>
 __device__ __forceinline__ void epilogue_piece(const Ops<FMT, CF> &o, int j, const v16i &D, const v16i &Dh,
-                                               float (&acc)[CF][16]) {
+                                               v16f (&acc)[CF]) {
     using O = Ops<FMT, CF>;
     const float wd = o.wd[j];
     const float wmn = O::HAS_MIN ? o.wm[O::HAS_MIN ? j : 0] : 0.0f;
@@ -268,7 +309,6 @@ __device__ __forceinline__ void epilogue_piece(const Ops<FMT, CF> &o, int j, con
 #pragma unroll
         for (int v = 0; v < 16; v++) {
             float t = __builtin_fmaf(__int_as_float(D[v]), wd, cd);
-            if (O::HAS_MIN) t = __builtin_fmaf(__int_as_float(o.av[O::HAS_MIN ? v : 0]), wmn, t);
             if (O::DUAL) t = t + __builtin_fmaf(__int_as_float(Dh[v]), wdh, cdh);
             acc[j][v] = __builtin_fmaf(t, o.xv[v], acc[j][v]);
         }
@@ -325,20 +365,31 @@ __device__ __forceinline__ void dots_piece(int j, const v16i &D, const v16i &Dh,
 // pipelined: block i+1's LDS operands are read before block i's epilogue, and
 // its MFMA for piece j is issued as soon as block i's epilogue has consumed
 // piece j's results, so the LDS and MFMA latencies of the next block overlap
-// the current block's VALU work.
+// the current block's VALU work. Q4_1 / Q5K1: the min terms of blocks i and
+// i + 1 go into acc (min_piece) at every even i.
 template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool PIPE, bool DBG>
 __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
-                                           const v16i &cmag, float (&acc)[CF][16], int *dots, int m0, int n0, int M,
-                                           int N, int G, int g0) {
+                                           const v16i &cmag, v16f (&acc)[CF], int *dots,
+                                           int m0, int n0, int M, int N, int G, int g0) {
+    constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    auto min_pair = [&](int i, MinOps<CF> &mo) {
+        load_min<FMT, KB, BM, BN, CF>(mo, S, blk0 + i * WK, i + 1 < NB ? blk0 + (i + 1) * WK : -1, wm, wn, lane);
+    };
     if (!PIPE) {
         // one block at a time (fewer registers: leaves room for a deeper global prefetch)
 #pragma unroll 1
         for (int i = 0; i < NB; i++) {
             Ops<FMT, CF> o;
             load_ops<FMT, KB, BM, BN, CF>(o, S, blk0 + i * WK, wm, wn, lane);
+            MinOps<CF> mo;
+            if (HAS_MIN && (i & 1) == 0) min_pair(i, mo);
             v16i D[CF], Dh[CF];
 #pragma unroll
             for (int j = 0; j < CF; j++) mfma_piece<FMT, CF>(o, j, cmag, D[j], Dh[j]);
+            if (HAS_MIN && (i & 1) == 0) {
+#pragma unroll
+                for (int j = 0; j < CF; j++) min_piece<CF>(mo, j, acc[j]);
+            }
 #pragma unroll
             for (int j = 0; j < CF; j++) {
                 if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
@@ -357,13 +408,21 @@ __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int 
         Ops<FMT, CF> &cur = ops[i & 1];
         Ops<FMT, CF> &nxt = ops[(i + 1) & 1];
         if (i + 1 < NB) load_ops<FMT, KB, BM, BN, CF>(nxt, S, blk0 + (i + 1) * WK, wm, wn, lane);
+        MinOps<CF> mo;
+        if (HAS_MIN && (i & 1) == 0) min_pair(i, mo);
         // keep the next block's LDS reads ahead of this block's epilogue
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < CF; j++) {
             if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
             epilogue_piece<FMT, CF, false>(cur, j, D[j], Dh[j], acc);
+            // fence the MFMA between two epilogue pieces: left to itself the
+            // scheduler sinks all of the next block's MFMAs below the last
+            // piece, and the next epilogue then waits out their latency
+            __builtin_amdgcn_sched_barrier(0);
             if (i + 1 < NB) mfma_piece<FMT, CF>(nxt, j, cmag, D[j], Dh[j]);
+            if (HAS_MIN && (i & 1) == 0) min_piece<CF>(mo, j, acc[j]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 }
@@ -371,12 +430,12 @@ __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int 
 // The same blocks in the reference's exact operation order, one at a time.
 template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool DBG>
 __device__ __forceinline__ void stage_slow(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
-                                           const v16i &cmag, float (&acc)[CF][16], int *dots, int m0, int n0, int M,
+                                           const v16i &cmag, v16f (&acc)[CF], int *dots, int m0, int n0, int M,
                                            int N, int G, int g0) {
 #pragma unroll 1
     for (int i = 0; i < NB; i++) {
         Ops<FMT, CF> o;
-        load_ops<FMT, KB, BM, BN, CF>(o, S, blk0 + i * WK, wm, wn, lane);
+        load_ops<FMT, KB, BM, BN, CF, true>(o, S, blk0 + i * WK, wm, wn, lane);
 #pragma unroll
         for (int j = 0; j < CF; j++) {
             v16i D, Dh;
@@ -421,7 +480,7 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
     const int nst = G / KB;
     const int st0 = sp * sps, st1 = min(nst, st0 + sps);
 
-    float acc[CF][16];
+    v16f acc[CF];
 #pragma unroll
     for (int j = 0; j < CF; j++)
 #pragma unroll
@@ -538,7 +597,6 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
 // with the fixed-order reduction when tiles are few.
 
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-typedef float v16f __attribute__((ext_vector_type(16)));
 
 constexpr int kQ5BM = 64;
 constexpr int kQ5Pieces = kQ5BM * 12;  // 16-byte pieces of a block-stage's activation parts
@@ -786,14 +844,17 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
 
 // Workgroup shapes of the int8 GEMM (4 waves of 32 x 64, 4-block K stages).
 // kWide: 64 x 128 tiles, the blocks of a stage software-pipelined, one stage
-// of global loads in flight. kDeep: 64 x 64 tiles, two waves per 32 x 64
+// of global loads in flight; kWide2: the same with two stages in flight
+// (for more than 128 rows: Q8_0 4096x14336 at M = 512 144.6 us against
+// 149.2, Q4_1 14336x4096 169.7 against 170.6; at M = 64 38.0 against 37.0
+// and 38.1 against 37.2). kDeep: 64 x 64 tiles, two waves per 32 x 64
 // taking alternate blocks of each stage, pipelined. kDeepS: kDeep computing
 // one block at a time, two stages of global loads in flight. kDeepS32: 32 x 64
 // tiles whose 4 waves take one block of each 4-block stage each (one block at
 // a time, two stages in flight), for Q5K1 with up to 32 activation rows (the
 // other formats measure faster on 64-row tiles even then: Q8_0 4096x14336 at
 // M = 32 on 32 x 256 tiles 46.8 us against 34.7 at M = 33 on kWide).
-enum GemmShape { kWide = 0, kDeep = 1, kDeepS = 2, kDeepS32 = 3 };
+enum GemmShape { kWide = 0, kDeep = 1, kDeepS = 2, kDeepS32 = 3, kWide2 = 4 };
 
 struct GemmPlan {
     int shape, bm, bn, kb, splits, sps, mtiles, ntiles;
@@ -825,7 +886,7 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
 }
 
 constexpr int shape_bm(int shape) { return shape == kDeepS32 ? 32 : 64; }
-constexpr int shape_bn(int shape) { return shape == kWide ? 128 : 64; }
+constexpr int shape_bn(int shape) { return shape == kWide || shape == kWide2 ? 128 : 64; }
 constexpr int shape_kb(int shape) { return 4; }
 
 GemmPlan plan_gemm(int fmt, int M, int N, int G) {
@@ -840,8 +901,8 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     // 100 / 168 / 575 (its wide tiles spill).
     // (Q5K1 with up to 32 activation rows: 32-row tiles; Q5K1 4096x4096 at M
     // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.)
-    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : kWide;
-    if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 4) p.shape = tuning().gemm_shape - 1;
+    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : (M > 128 ? kWide2 : kWide);
+    if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 5) p.shape = tuning().gemm_shape - 1;
     p.bm = shape_bm(p.shape);
     p.bn = shape_bn(p.shape);
     p.kb = shape_kb(p.shape);
@@ -879,6 +940,7 @@ sllm_status launch_fmt(const Planes &P, const int8_t *xq, const float *xsp, cons
     case kDeep: return launch_shape<FMT, 2, 1, 2, 2, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     case kDeepS: return launch_shape<FMT, 2, 1, 2, 2, 4, false, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     case kDeepS32: return launch_shape<FMT, 1, 1, 2, 4, 4, false, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case kWide2: return launch_shape<FMT, 2, 2, 2, 1, 4, true, 2, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     default: return launch_shape<FMT, 2, 2, 2, 1, 4, true, 1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     }
 }

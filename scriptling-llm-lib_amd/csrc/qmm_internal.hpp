@@ -259,7 +259,7 @@ struct Tuning {
     int gemv_max_nb = 8;       // max blocks per lane in one GEMV unit (K-chunk)
     int gemv_inflight_kb = 32768;  // weight bytes in flight over the device (ring depth)
     int gemm_min_rows = 0;     // xRows at which the MFMA GEMM takes over (0: 8, or 16 below 2^24 weights)
-    int gemm_shape = 0;        // GEMM workgroup shape (1..3; 0: by format)
+    int gemm_shape = 0;        // GEMM workgroup shape (1..5; 0: by format and rows)
     int gemm_splits = 0;       // GEMM K splits (0: by tile count)
     int gemv_q4k_stream = 0;   // load option: Q4_K weights keep (and stream) the GGUF headers (1) or not (0, faster)
     int gemv_q6k_stream = 0;   // load option: Q6_K weights keep (and stream) the native 6-bit planes (1) or not (0)

@@ -1,7 +1,8 @@
-"""GPU parity of the prefill path (xRows >= 64: int8 MFMA GEMM; Q5_0 stays on
-the GEMV) against the oracle, including full BASELINE C4 shapes checked on a
-row subset (weight rows are independent, so a row slice of the Raw bytes is
-the oracle's input for those output columns)."""
+"""GPU parity of the prefill path (from 8 or 16 activation rows: the int8 MFMA
+GEMM for Q8_0 / Q4_0 / Q4_1 / Q5K1, the bf16 MFMA GEMM for Q5_0) against the
+oracle, including full BASELINE C4 shapes checked on a row subset (weight rows
+are independent, so a row slice of the Raw bytes is the oracle's input for
+those output columns), and the GEMM's int32 block dots bit for bit."""
 from __future__ import annotations
 
 import numpy as np
@@ -44,7 +45,7 @@ def test_prefill_parity(qtype, M, N, K):
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
 @pytest.mark.parametrize("shape,splits", [(1, 1), (1, 3), (2, 5), (2, 8), (1, 2), (2, 1), (3, 1), (3, 3), (3, 8),
-                                          (4, 1), (4, 3)])
+                                          (4, 1), (4, 3), (5, 1), (5, 3), (5, 8)])
 def test_shape_and_split_overrides(qtype, shape, splits):
     # every workgroup shape and any K split count gives the oracle's result
     # within the bound (K = 1024 is 8 stages: 5 splits of 2 stages leave the
@@ -82,7 +83,7 @@ def _block_dots_case(qtype, raw, N, K, x, row0, n_rows, shape=0):
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
 @pytest.mark.parametrize("M", [64, 130])
-@pytest.mark.parametrize("shape", [1, 2, 3, 4])
+@pytest.mark.parametrize("shape", [1, 2, 3, 4, 5])
 def test_gemm_block_dots_bitexact(qtype, M, shape):
     # the int32 block dots the matrix cores return, read from the registers the
     # epilogue scales, against the oracle's per-(row, block) dots
@@ -107,6 +108,29 @@ def test_gemm_block_dots_c3_gate_rows(M):
     got = sq.debug_gemm_block_dots(w, x, N - 256, 256)
     sub = slice_rows("q4_1", raw, N, K // 32, np.arange(N - 256, N))
     assert np.array_equal(got, oracle.block_dots("q4_1", sub, 256, K, x))
+
+
+@pytest.mark.parametrize("qtype", ["q4_1", "q5k1"])
+@pytest.mark.parametrize("shape", [0, 4])
+def test_gemm_min_term_dominant(qtype, shape):
+    # mins far larger than scale x code, of both signs: the min term (added on
+    # the fp32 matrix cores two blocks at a time, one block on the 32-row
+    # tiles of shape 4) carries most of each output
+    N, K, M = 160, 1024, 72
+    G = K // 32
+    raw = make_raw(qtype, N, K, seed=31).copy()
+    blocks = raw[: N * G * 20].reshape(N * G, 20)
+    m = np.random.default_rng(5).uniform(-64.0, 64.0, N * G).astype(np.float16)
+    blocks[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, G, N, K))
+    x = make_x(M, K, seed=32)
+    sq.set_param("gemm_shape", shape)
+    try:
+        got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    finally:
+        sq.set_param("gemm_shape", 0)
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} dominant mins")
 
 
 @pytest.mark.parametrize("qtype", ["q8", "q4", "q4_1", "q5k1"])
