@@ -217,6 +217,18 @@ __device__ __forceinline__ int bits_isum(uint32_t hb, int4 xl, int4 xh) {
     return s;
 }
 
+// Signed Q5_0 codes q5 - 16 of four elements as bytes: the nibble (low four
+// bits of each byte of nib), with 0xf0 above it where the element's high bit
+// is clear (bits b0..b3 of clear4), i.e. the nibble - 16. 255 t (t: 0 / 1
+// bytes) is formed as (t << 8) - t: a 32-bit multiply runs at a quarter of
+// the VALU rate.
+__device__ __forceinline__ uint32_t q5_codes(uint32_t nib, uint32_t clear4) {
+    const uint32_t t = (uint32_t)spread4(clear4);
+    uint32_t t8 = t << 8;
+    asm("" : "+v"(t8));
+    return (nib & 0x0f0f0f0fu) | ((t8 - t) & 0xf0f0f0f0u);
+}
+
 // Q5_0 in-block fp32 partial sum in the reference order (q5DotGroupXF32,
 // float32_ops.go:335-367): sum += v0*x[j] + v1*x[j+16] for j = 0..15, with
 // v = float(q5) - 16 and q5 = nibble | (bit e of qh) << 4. xb holds the block's
@@ -234,8 +246,8 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
         // the nibble, with 0xf0 above it where the high bit is clear (the
         // nibble - 16), so each converts with one sign-extending byte-to-float
         // instruction; float(q5 - 16) is float(q5) - 16 exactly (+0 for 16)
-        const uint32_t lo = (w[jj] & 0x0f0f0f0fu) | ((uint32_t)spread4(~qh >> (4 * jj)) * 0xf0u);
-        const uint32_t hi = ((w[jj] >> 4) & 0x0f0f0f0fu) | ((uint32_t)spread4(~qh >> (16 + 4 * jj)) * 0xf0u);
+        const uint32_t lo = q5_codes(w[jj], ~qh >> (4 * jj));
+        const uint32_t hi = q5_codes(w[jj] >> 4, ~qh >> (16 + 4 * jj));
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             float v0 = (float)(int)(int8_t)((lo >> (8 * k)) & 0xffu);
@@ -247,6 +259,32 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
         }
     }
     return sum;
+}
+
+// The same block sum reassociated for the GEMV: the products of elements j
+// and j + 16 go into two fused multiply-add chains (16 steps each, one
+// rounding per step) that are added at the end - about 2 VALU operations per
+// weight instead of 3, the two chains overlapping. The products v * x are
+// the reference's; only the order of the additions and their rounding differ
+// (each partial is within a few ulp of the block's sum |v x|).
+__device__ __forceinline__ float q5_block_sum_fma(int4 q, uint32_t qh, const float4 *xb) {
+    const uint32_t w[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+        float4 a = xb[jj];
+        float4 b = xb[jj + 4];
+        const float av[4] = {a.x, a.y, a.z, a.w};
+        const float bv[4] = {b.x, b.y, b.z, b.w};
+        const uint32_t lo = q5_codes(w[jj], ~qh >> (4 * jj));
+        const uint32_t hi = q5_codes(w[jj] >> 4, ~qh >> (16 + 4 * jj));
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            s0 = __builtin_fmaf((float)(int)(int8_t)((lo >> (8 * k)) & 0xffu), av[k], s0);
+            s1 = __builtin_fmaf((float)(int)(int8_t)((hi >> (8 * k)) & 0xffu), bv[k], s1);
+        }
+    }
+    return s0 + s1;
 }
 
 // ------------------------------------------------------ wave reduction ----

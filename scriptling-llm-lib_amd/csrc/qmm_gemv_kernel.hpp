@@ -299,7 +299,7 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
         t = t * x.xs;
         acc = acc + t;
     } else if (FMT == SLLM_Q5_0) {
-        const float sum = q5_block_sum(b.q, b.qh, x.xf);
+        const float sum = q5_block_sum_fma(b.q, b.qh, x.xf);
         const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`
         acc = acc + grp;
     } else if (FMT == SLLM_Q8_0) {
@@ -803,8 +803,10 @@ template <int FMT, int NB, int D, int MT, bool PAIR>
 sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, int RPW, int W, int grid,
                      size_t lds, hipStream_t s) {
     // hoisting needs room for the operands: fp32-activation formats hold 32
-    // floats per block (not for Q5_0, whose term needs more registers itself)
-    constexpr bool kCanHoist = act_f32(FMT) ? (kq_native(FMT) && NB * MT <= 2 && NB * D <= 2) : NB * MT <= 4;
+    // floats per block
+    constexpr bool kCanHoist = act_f32(FMT) ? ((kq_native(FMT) || FMT == SLLM_Q5_0) && NB * MT <= 2 &&
+                                               NB * D <= (FMT == SLLM_Q5_0 ? 4 : 2))
+                                            : NB * MT <= 4;
     // lanes per activation block in the prologue: 8 where the workgroup allows,
     // 4 with the RMSNorm in front and where a wave streams at most two units
     // (the waves left without an activation block issue their whole ring at
