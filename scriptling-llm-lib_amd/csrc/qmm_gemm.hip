@@ -501,7 +501,7 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
                                                               st * KB);
     };
     using Fe = Fetch<FMT, KB, BM, BN, T>;
-    if (PF == 1) {
+    if constexpr (PF == 1) {
         Fe f;
         if (st0 < st1) {
             fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
@@ -658,7 +658,7 @@ struct alignas(16) Q5Stage {
 template <int T>
 struct Q5Fetch {
     static constexpr int A_PER = (kQ5Pieces + T - 1) / T;
-    int4 a[A_PER];
+    v4i a[A_PER];  // a native vector: an array of HIP's int4 (a union) is kept in scratch memory
     uint2 qs;
     uint32_t qh;
     uint16_t d;
@@ -670,12 +670,13 @@ __device__ __forceinline__ void q5m_fetch(Q5Fetch<T> &f, const Planes &P, const 
     const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < Q5Fetch<T>::A_PER; i++) {
-        const int e = t + T * i;  // piece e: row e / 12, part (e % 12) / 4, 16 bytes e % 4
-        if (kQ5Pieces % T == 0 || e < kQ5Pieces) {
-            const int m = min(m0 + e / 12, M - 1);  // rows past M reload the last row; never stored
-            const int rem = e % 12;
-            f.a[i] = *(const int4 *)(xs3 + ((size_t)m * G + g) * 96 + (rem >> 2) * 32 + (rem & 3) * 8);
-        }
+        // piece e: row e / 12, part (e % 12) / 4, 16 bytes e % 4; a thread past
+        // the last piece reloads it (never stored): the loads stay unconditional,
+        // so the array stays in registers
+        const int e = min(t + T * i, kQ5Pieces - 1);
+        const int m = min(m0 + e / 12, M - 1);  // rows past M reload the last row; never stored
+        const int rem = e % 12;
+        f.a[i] = *(const v4i *)(xs3 + ((size_t)m * G + g) * 96 + (rem >> 2) * 32 + (rem & 3) * 8);
     }
     const int n = min(n0 + (t >> 1), N - 1);
     const size_t idx = (size_t)n * G + g;
@@ -695,7 +696,7 @@ __device__ __forceinline__ void q5m_store(const Q5Fetch<T> &f, Q5Stage<T / 2> &S
         const int e = t + T * i;
         if (kQ5Pieces % T == 0 || e < kQ5Pieces) {
             const int rem = e % 12;
-            *(int4 *)&S.a[rem >> 2][e / 12][(rem & 3) * 8] = f.a[i];
+            *(v4i *)&S.a[rem >> 2][e / 12][(rem & 3) * 8] = f.a[i];
         }
     }
     // weight row t / 2: nibble bytes 8 h .. 8 h + 7 hold elements j (low) and
@@ -726,28 +727,29 @@ __device__ __forceinline__ void q5m_store(const Q5Fetch<T> &f, Q5Stage<T / 2> &S
 // One block's MFMAs and epilogue for one wave's 32 x 64 tile.
 template <int BN>
 __device__ __forceinline__ void q5m_block(const Q5Stage<BN> &S, int wm, int wn, int r32, int h, float (&acc)[2][16]) {
-    // operands: step s covers elements 16 s .. 16 s + 15, lane half h 8 of them
-    v8bf a[3][2], b[2][2];
+    // operands of one step at a time (step s: elements 16 s .. 16 s + 15, lane
+    // half h 8 of them): the whole block's would hold 40 registers, and at 4
+    // waves per SIMD the global prefetch then spills
+    v16f sum[2] = {};
 #pragma unroll
     for (int s2 = 0; s2 < 2; s2++) {
+        v8bf a[3], b[2];
 #pragma unroll
         for (int part = 0; part < 3; part++)
-            a[part][s2] = __builtin_bit_cast(v8bf, *(const int4 *)&S.a[part][wm * 32 + r32][16 * s2 + 8 * h]);
+            a[part] = __builtin_bit_cast(v8bf, *(const int4 *)&S.a[part][wm * 32 + r32][16 * s2 + 8 * h]);
 #pragma unroll
         for (int j = 0; j < 2; j++)
-            b[j][s2] = __builtin_bit_cast(v8bf, *(const int4 *)&S.b[wn * 64 + 32 * j + r32][16 * s2 + 8 * h]);
+            b[j] = __builtin_bit_cast(v8bf, *(const int4 *)&S.b[wn * 64 + 32 * j + r32][16 * s2 + 8 * h]);
+#pragma unroll
+        for (int part = 0; part < 3; part++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) sum[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[part], b[j], sum[j], 0, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
-        v16f sum = {};
-#pragma unroll
-        for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-            for (int part = 0; part < 3; part++)
-                sum = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[part][s2], b[j][s2], sum, 0, 0, 0);
         const float dd = S.d[wn * 64 + 32 * j + r32];
 #pragma unroll
-        for (int v = 0; v < 16; v++) acc[j][v] = __builtin_fmaf(dd, sum[v], acc[j][v]);
+        for (int v = 0; v < 16; v++) acc[j][v] = __builtin_fmaf(dd, sum[j][v], acc[j][v]);
     }
 }
 
@@ -784,7 +786,7 @@ __global__ void __launch_bounds__(128 * WN) gemm_q5_kernel(Planes P, const uint1
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[j][v] = 0.0f;
 
-    if (PF == 1) {
+    if constexpr (PF == 1) {
         Q5Fetch<T> f;
         if (g0 < g1) {
             q5m_fetch(f, P, xs3, M, N, G, m0, n0, g0);
@@ -845,9 +847,10 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
 // Workgroup shapes of the int8 GEMM (4 waves of 32 x 64, 4-block K stages).
 // kWide: 64 x 128 tiles, the blocks of a stage software-pipelined, one stage
 // of global loads in flight; kWide2: the same with two stages in flight
-// (for more than 128 rows: Q8_0 4096x14336 at M = 512 144.6 us against
-// 149.2, Q4_1 14336x4096 169.7 against 170.6; at M = 64 38.0 against 37.0
-// and 38.1 against 37.2). kDeep: 64 x 64 tiles, two waves per 32 x 64
+// (Q8_0 / Q4_0 above 128 rows: Q8_0 4096x14336 at M = 512 144.6 us against
+// 149.2, at M = 64 38.0 against 37.0; Q4_1 14336x4096 169.7 against 170.6
+// at M = 512, and its second register set spills, so Q4_1 stays on kWide).
+// kDeep: 64 x 64 tiles, two waves per 32 x 64
 // taking alternate blocks of each stage, pipelined. kDeepS: kDeep computing
 // one block at a time, two stages of global loads in flight. kDeepS32: 32 x 64
 // tiles whose 4 waves take one block of each 4-block stage each (one block at
@@ -866,11 +869,12 @@ GemmPlan plan_gemm_q5(int M, int N, int G) {
     p.shape = 0;
     p.bm = kQ5BM;
     // 64 x 256 tiles (8 waves) halve the activation parts' re-reads across
-    // N-tiles: 14336x4096 at M = 16 / 64 / 128 / 512 82.6 / 93.9 / 155.1 /
-    // 456.5 us against 95.7 / 107.2 / 183.3 / 644.7 on 64 x 128 tiles (4
-    // waves), which stay ahead for narrow weights at few rows (1024x4096 at
-    // M = 16 / 64 / 128: 24.1 / 27.3 / 32.1 against 27.2 / 29.7 / 34.4)
-    p.bn = (N >= 4096 || M > 128) ? 256 : 128;
+    // N-tiles: 14336x4096 at M = 16 / 64 / 128 / 512 54.7 / 60.9 / 106.5 /
+    // 357.3 us against 58.5 / 65.3 / 119.8 / 397.3 on 64 x 128 tiles (4
+    // waves), which stay ahead up to 4096 weight rows at few activation rows
+    // (4096x4096 at M = 16 / 64 / 128: 26.1 / 30.2 / 38.9 against 30.0 / 33.3
+    // / 39.5; 1024x4096: 20.8 / 25.2 / 27.4 against 22.3 / 26.2 / 31.6)
+    p.bn = (N > 4096 || M > 128) ? 256 : 128;
     if (tuning().gemm_shape == 1) p.bn = 256;
     if (tuning().gemm_shape == 2) p.bn = 128;
     p.kb = 1;
@@ -901,7 +905,8 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     // 100 / 168 / 575 (its wide tiles spill).
     // (Q5K1 with up to 32 activation rows: 32-row tiles; Q5K1 4096x4096 at M
     // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.)
-    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : (M > 128 ? kWide2 : kWide);
+    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS)
+                               : (M > 128 && fmt != SLLM_Q4_1 ? kWide2 : kWide);
     if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 5) p.shape = tuning().gemm_shape - 1;
     p.bm = shape_bm(p.shape);
     p.bn = shape_bn(p.shape);
