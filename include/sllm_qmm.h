@@ -355,6 +355,14 @@ sllm_status sllm_matmul_swiglu_into_f32(const sllm_weight *w_gate, const sllm_we
  * graph captured on stream S keeps S's scratch wherever it is replayed: a
  * replay must not overlap an argmax launch on S, nor a replay of another
  * graph captured on S (the shared counter would misfire).
+ * Ordering assumption: the workgroups combine their maxima with device-scope
+ * relaxed atomics and no fence (a fence writes back and invalidates the L2 of
+ * each XCD). The last workgroup to count reads every maximum because a
+ * device-scope read-modify-write whose old value has returned has been
+ * performed at the device's coherence point, and each workgroup counts only
+ * after its maximum has returned. This holds on gfx950 (the argmax tests
+ * check ties, NaN rules, repeated launches, two streams and graph replays)
+ * but is not promised by the HIP memory model for relaxed atomics.
  */
 sllm_status sllm_matmul_argmax_dev(const sllm_weight *w, const float *x_dev, int x_cols, float *logits_dev,
                                    int *argmax_dev, void *stream);
