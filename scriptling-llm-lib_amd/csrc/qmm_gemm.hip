@@ -45,9 +45,11 @@
 //
 // MFMA operand layout (32x32x32 i8): A row i in lanes i and i + 32, 16 bytes
 // each; B column j in lanes j and j + 32; D[i][j] in lane j + 32 h, element
-// 4 q + r for i = 8 q + 4 h + r. A block's 32 codes are stored in LDS in the
-// order (0..7, 16..23, 8..15, 24..31), so lane half h reads its 16 bytes with
-// one ds_read_b128 and both operands pair the same elements.
+// 4 q + r for i = 8 q + 4 h + r. A block's 32 codes are stored in LDS in
+// element order and lane half h reads elements 16 h .. 16 h + 15 with one
+// ds_read_b128, for both operands: whatever k each byte position stands for
+// inside the instruction, both operands pair the same elements, and an int32
+// dot does not depend on the order of its products.
 #include <hip/hip_runtime.h>
 
 #include "qmm_device.hpp"
@@ -89,8 +91,9 @@ struct Fetch {
     static constexpr int A_N = BM * KB, B_N = BN * KB;
     static constexpr int A_PER = (A_N + T - 1) / T, B_PER = (B_N + T - 1) / T;
     static constexpr bool Q8 = FMT == SLLM_Q8_0;
-    int4 a[A_PER][2];
-    int4 b[B_PER][Q8 ? 2 : 1];
+    // native vectors: an array of HIP's int4 (a union) copied whole is kept in scratch memory
+    v4i a[A_PER][2];
+    v4i b[B_PER][Q8 ? 2 : 1];
     float xs[A_PER];
     int sx[A_PER];
     uint16_t d[B_PER], m[B_PER], dh[B_PER];
@@ -110,7 +113,7 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
         const int e = tid + T * i;
         if (F::A_N % T == 0 || e < F::A_N) {
             const int m = min(m0 + e / KB, M - 1);  // rows past M reload the last row; never stored
-            const int4 *p = (const int4 *)(xq + (size_t)m * K + (size_t)(g0 + e % KB) * 32);
+            const v4i *p = (const v4i *)(xq + (size_t)m * K + (size_t)(g0 + e % KB) * 32);
             f.a[i][0] = p[0];
             f.a[i][1] = p[1];
             const size_t si = (size_t)m * G + g0 + e % KB;
@@ -124,8 +127,8 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
         if (F::B_N % T == 0 || e < F::B_N) {
             const int n = min(n0 + e / KB, N - 1);
             const size_t idx = (size_t)n * G + g0 + e % KB;
-            f.b[i][0] = P.qs[idx];
-            if (F::Q8) f.b[i][F::Q8 ? 1 : 0] = P.qs2[idx];
+            f.b[i][0] = *(const v4i *)(P.qs + idx);
+            if (F::Q8) f.b[i][F::Q8 ? 1 : 0] = *(const v4i *)(P.qs2 + idx);
             f.d[i] = P.d[idx];
             if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) f.m[i] = P.m[idx];
             if (FMT == SLLM_Q5K1) {
@@ -157,11 +160,9 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
         const int e = tid + T * i;
         if (F::A_N % T == 0 || e < F::A_N) {
             const int r = e / KB, blk = e % KB;
-            // elements 0..15 = (x, y | z, w), 16..31 = (x, y | z, w) of the second int4
-            const int4 lo = f.a[i][0], hi = f.a[i][1];
-            int4 *p = (int4 *)(S.a + r * RB + blk * 32);
-            p[0] = make_int4(lo.x, lo.y, hi.x, hi.y);
-            p[1] = make_int4(lo.z, lo.w, hi.z, hi.w);
+            v4i *p = (v4i *)(S.a + r * RB + blk * 32);
+            p[0] = f.a[i][0];  // elements 0..15
+            p[1] = f.a[i][1];  // elements 16..31
             S.xs[blk][r] = f.xs[i];
             if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) S.aux[blk][r] = __float_as_int((float)f.sx[i]);
             slow |= !(f.xs[i] < kHugeXs);
@@ -172,24 +173,24 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
         const int e = tid + T * i;
         if (F::B_N % T == 0 || e < F::B_N) {
             const int r = e / KB, blk = e % KB;
-            int4 *p = (int4 *)(S.b + r * RB + blk * 32);
+            v4i *p = (v4i *)(S.b + r * RB + blk * 32);
             if (F::Q8) {
-                const int4 lo = f.b[i][0], hi = f.b[i][F::Q8 ? 1 : 0];
-                p[0] = make_int4(lo.x, lo.y, hi.x, hi.y);
-                p[1] = make_int4(lo.z, lo.w, hi.z, hi.w);
+                p[0] = f.b[i][0];
+                p[1] = f.b[i][F::Q8 ? 1 : 0];
             } else {
                 // byte j holds element j (low nibble) and element j + 16 (high nibble)
-                const int4 v = f.b[i][0];
-                int c[8] = {v.x & 0x0f0f0f0f, v.y & 0x0f0f0f0f, (v.x >> 4) & 0x0f0f0f0f, (v.y >> 4) & 0x0f0f0f0f,
-                            v.z & 0x0f0f0f0f, v.w & 0x0f0f0f0f, (v.z >> 4) & 0x0f0f0f0f, (v.w >> 4) & 0x0f0f0f0f};
+                const v4i v = f.b[i][0];
+                int c[8] = {v.x & 0x0f0f0f0f,        v.y & 0x0f0f0f0f,        v.z & 0x0f0f0f0f,
+                            v.w & 0x0f0f0f0f,        (v.x >> 4) & 0x0f0f0f0f, (v.y >> 4) & 0x0f0f0f0f,
+                            (v.z >> 4) & 0x0f0f0f0f, (v.w >> 4) & 0x0f0f0f0f};
                 if (FMT == SLLM_Q4_0) {
                     // the signed code nib - 8 per byte (q4q8.go:37-43): 0x80 + nib - 8 never
                     // borrows across bytes, and ^ 0x80 gives (nib - 8) mod 256
 #pragma unroll
                     for (int k = 0; k < 8; k++) c[k] = ((c[k] | (int)0x80808080) - 0x08080808) ^ (int)0x80808080;
                 }
-                p[0] = make_int4(c[0], c[1], c[2], c[3]);
-                p[1] = make_int4(c[4], c[5], c[6], c[7]);
+                p[0] = v4i{c[0], c[1], c[2], c[3]};
+                p[1] = v4i{c[4], c[5], c[6], c[7]};
             }
             S.d[blk][r] = (FMT == SLLM_Q8_0) ? f16_lut(f.d[i]) : f16_exact(f.d[i]);
             slow |= f16_nonfinite(f.d[i]);
@@ -204,8 +205,8 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
                 int4 *q = (int4 *)(S.bh + r * RB + blk * 32);
                 const int2 c0 = spread8(hb & 0xffu), c1 = spread8((hb >> 8) & 0xffu);
                 const int2 c2 = spread8((hb >> 16) & 0xffu), c3 = spread8(hb >> 24);
-                q[0] = make_int4(c0.x, c0.y, c2.x, c2.y);
-                q[1] = make_int4(c1.x, c1.y, c3.x, c3.y);
+                q[0] = make_int4(c0.x, c0.y, c1.x, c1.y);
+                q[1] = make_int4(c2.x, c2.y, c3.x, c3.y);
             }
         }
     }
