@@ -433,8 +433,8 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
  *                                  each K stage split over two waves, 3 = as 2 with two
  *                                  stages of loads in flight, 4 = 32 x 64 tiles with each
  *                                  stage split over four waves, 5 = as 1 with two stages of
- *                                  loads in flight (0: 1, for Q8_0 / Q4_0 above 128 rows 5,
- *                                  for Q5K1 3, and 4 up to 32 rows); Q5_0: 1 = 64 x 256
+ *                                  loads in flight (0: 1, above 128 rows 5; for Q5K1 3,
+ *                                  and 4 up to 32 rows); Q5_0: 1 = 64 x 256
  *                                  tiles, 2 = 64 x 128 (0: 2 up to 4096 weight rows and
  *                                  128 activation rows, else 1). The shape moves the fp32
  *                                  summation splits

@@ -847,11 +847,11 @@ __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__re
 
 // Workgroup shapes of the int8 GEMM (4 waves of 32 x 64, 4-block K stages).
 // kWide: 64 x 128 tiles, the blocks of a stage software-pipelined, one stage
-// of global loads in flight; kWide2: the same with two stages in flight
-// (Q8_0 / Q4_0 above 128 rows: Q8_0 4096x14336 at M = 512 144.6 us against
-// 149.2, at M = 64 38.0 against 37.0; Q4_1 14336x4096 169.7 against 170.6
-// at M = 512, and its second register set spills, so Q4_1 stays on kWide).
-// kDeep: 64 x 64 tiles, two waves per 32 x 64
+// of global loads in flight; kWide2: the same with two stages in flight, for
+// more than 128 rows (Q8_0 4096x14336 at M = 256 / 512 / 1024 79.6 / 139.1 /
+// 245.6 us against 82.8 / 143.8 / 254.9, Q4_1 14336x4096 89.9 / 162.4 /
+// 289.7 against 91.0 / 167.1 / 287.7; at M = 64 35.1 against 33.6 and 37.3
+// against 34.5). kDeep: 64 x 64 tiles, two waves per 32 x 64
 // taking alternate blocks of each stage, pipelined. kDeepS: kDeep computing
 // one block at a time, two stages of global loads in flight. kDeepS32: 32 x 64
 // tiles whose 4 waves take one block of each 4-block stage each (one block at
@@ -906,8 +906,7 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     // 100 / 168 / 575 (its wide tiles spill).
     // (Q5K1 with up to 32 activation rows: 32-row tiles; Q5K1 4096x4096 at M
     // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.)
-    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS)
-                               : (M > 128 && fmt != SLLM_Q4_1 ? kWide2 : kWide);
+    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : (M > 128 ? kWide2 : kWide);
     if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 5) p.shape = tuning().gemm_shape - 1;
     p.bm = shape_bm(p.shape);
     p.bn = shape_bn(p.shape);
