@@ -437,9 +437,10 @@ def gemm_probe(sq, synth, torch, stream) -> int:
               ("q8 down", lambda: mk(synth.GGML_Q6_K, synth.q6k_blocks(102, H, F), H, F)),
               ("q5k1 q/o", lambda: mk(synth.GGML_Q5_K, synth.q5k_blocks(21, H, H), H, H)),
               ("q5k1 ffn", lambda: mk(synth.GGML_Q5_K, synth.q5k_blocks(22, F, H), F, H))]
-    wf = synth.normal(30, H * H, 0.02).reshape(H, H)
-    q5raw = synth.quantize_q5_0(wf)
+    q5raw = synth.quantize_q5_0(synth.normal(30, H * H, 0.02).reshape(H, H))
     shapes.append(("q5 q/o", lambda: sq.DeviceWeight.from_quant(sq.QuantWeight("q5", q5raw, H // 32, H, H))))
+    q5raw_f = synth.quantize_q5_0(synth.normal(31, F * H, 0.02).reshape(F, H))
+    shapes.append(("q5 ffn", lambda: sq.DeviceWeight.from_quant(sq.QuantWeight("q5", q5raw_f, H // 32, F, H))))
     xs = {c: torch.from_numpy(synth.normal(7, 512 * c)).cuda() for c in (H, F)}
     y = torch.empty(512 * F, device="cuda")
     for name, make in shapes:
