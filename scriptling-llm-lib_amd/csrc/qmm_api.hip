@@ -11,6 +11,7 @@
 #include <unordered_map>
 #include <vector>
 
+#include "qmm_device.hpp"
 #include "qmm_internal.hpp"
 
 struct sllm_weight {
@@ -927,8 +928,9 @@ sllm_status sllm_weight_export(const sllm_weight *w, void *raw, size_t cap) {
             std::memcpy(lo + 4, &p.qs[b], 16);
             put16(hi, p.dh[b]);
             put16(hi + 2, 0);
+            const uint32_t bits = q5k1_groups_to_bits(p.qh[b]);  // bit e = element e
             for (int i = 0; i < 16; i++)
-                hi[4 + i] = (unsigned char)(((p.qh[b] >> i) & 1u) | (((p.qh[b] >> (i + 16)) & 1u) << 4));
+                hi[4 + i] = (unsigned char)(((bits >> i) & 1u) | (((bits >> (i + 16)) & 1u) << 4));
             break;
         }
         }

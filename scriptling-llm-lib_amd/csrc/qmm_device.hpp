@@ -204,16 +204,34 @@ __device__ __forceinline__ int nib_isum(int4 q, int4 xl, int4 xh) {
 // Four bits (b0..b3 of t) -> four bytes holding 0 or 1.
 __device__ __forceinline__ int spread4(uint32_t t) { return (int)(((t & 0xfu) * 0x00204081u) & 0x01010101u); }
 
-// Σ bit_e·xq_e for a 32-bit mask (bit e = element e): the Q5K1 high block.
+// The Q5K1 high-bit word is kept in group order: bit 8 i + k holds the high
+// bit of element 4 k + i (i < 4, k < 8), so (w >> k) & 0x01010101 spreads the
+// four elements of group k to bytes with one shift and one mask.
+__host__ __device__ inline uint32_t q5k1_bits_to_groups(uint32_t bits) {
+    uint32_t g = 0;
+    for (int k = 0; k < 8; k++)
+        for (int i = 0; i < 4; i++) g |= ((bits >> (4 * k + i)) & 1u) << (8 * i + k);
+    return g;
+}
+__host__ __device__ inline uint32_t q5k1_groups_to_bits(uint32_t g) {
+    uint32_t bits = 0;
+    for (int k = 0; k < 8; k++)
+        for (int i = 0; i < 4; i++) bits |= ((g >> (8 * i + k)) & 1u) << (4 * k + i);
+    return bits;
+}
+
+// Σ bit_e·xq_e over a block's 32 elements, the high bits in group order: the
+// Q5K1 high block.
 __device__ __forceinline__ int bits_isum(uint32_t hb, int4 xl, int4 xh) {
-    int s = dot4(spread4(hb), xl.x, 0);
-    s = dot4(spread4(hb >> 4), xl.y, s);
-    s = dot4(spread4(hb >> 8), xl.z, s);
-    s = dot4(spread4(hb >> 12), xl.w, s);
-    s = dot4(spread4(hb >> 16), xh.x, s);
-    s = dot4(spread4(hb >> 20), xh.y, s);
-    s = dot4(spread4(hb >> 24), xh.z, s);
-    s = dot4(spread4(hb >> 28), xh.w, s);
+    constexpr uint32_t m = 0x01010101u;
+    int s = dot4((int)(hb & m), xl.x, 0);
+    s = dot4((int)((hb >> 1) & m), xl.y, s);
+    s = dot4((int)((hb >> 2) & m), xl.z, s);
+    s = dot4((int)((hb >> 3) & m), xl.w, s);
+    s = dot4((int)((hb >> 4) & m), xh.x, s);
+    s = dot4((int)((hb >> 5) & m), xh.y, s);
+    s = dot4((int)((hb >> 6) & m), xh.z, s);
+    s = dot4((int)((hb >> 7) & m), xh.w, s);
     return s;
 }
 

@@ -141,11 +141,6 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
 
 __device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7c00u) == 0x7c00u; }
 
-// 8 bits -> 8 bytes of 0 / 1 (bit i -> byte i).
-__device__ __forceinline__ int2 spread8(uint32_t b) {
-    return make_int2(spread4(b & 0xfu), spread4((b >> 4) & 0xfu));
-}
-
 // Stores the fetched stage `stage` into LDS in the MFMA's element order; a
 // thread that sees a scale needing the exact epilogue writes `stage` to S.tag.
 template <int FMT, int KB, int BM, int BN, int T>
@@ -201,12 +196,12 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
             if (FMT == SLLM_Q5K1) {
                 S.dh[FMT == SLLM_Q5K1 ? blk : 0][r] = f16_exact(f.dh[i]);
                 slow |= f16_nonfinite(f.dh[i]);
-                const uint32_t hb = f.hb[i];  // bit e = high bit of element e
-                int4 *q = (int4 *)(S.bh + r * RB + blk * 32);
-                const int2 c0 = spread8(hb & 0xffu), c1 = spread8((hb >> 8) & 0xffu);
-                const int2 c2 = spread8((hb >> 16) & 0xffu), c3 = spread8(hb >> 24);
-                q[0] = make_int4(c0.x, c0.y, c1.x, c1.y);
-                q[1] = make_int4(c2.x, c2.y, c3.x, c3.y);
+                // high bits in group order: (hb >> k) & 0x01010101 = elements 4k .. 4k + 3
+                const int hb = (int)f.hb[i];
+                constexpr int m = 0x01010101;
+                v4i *q = (v4i *)(S.bh + r * RB + blk * 32);
+                q[0] = v4i{hb & m, (hb >> 1) & m, (hb >> 2) & m, (hb >> 3) & m};
+                q[1] = v4i{(hb >> 4) & m, (hb >> 5) & m, (hb >> 6) & m, (hb >> 7) & m};
             }
         }
     }

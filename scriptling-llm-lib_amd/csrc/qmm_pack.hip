@@ -180,7 +180,7 @@ __global__ void pack_raw_kernel(int fmt, const uint8_t *__restrict__ raw, int64_
                 bits |= (v & 1u) << i;
                 bits |= ((v >> 4) & 1u) << (i + 16);
             }
-            P.qh[b] = bits;
+            P.qh[b] = q5k1_bits_to_groups(bits);
             if (bad) *err = 1;
             break;
         }
@@ -212,7 +212,7 @@ __global__ void pack_q5k_kernel(const uint8_t *__restrict__ raw, int64_t nb, Mut
             bits |= (uint32_t)((qh[i] >> jj) & 1) << i;
             bits |= (uint32_t)((qh[i + 16] >> jj) & 1) << (i + 16);
         }
-        P.qh[b] = bits;
+        P.qh[b] = q5k1_bits_to_groups(bits);
     }
 }
 
