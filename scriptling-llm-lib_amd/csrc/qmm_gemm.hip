@@ -100,7 +100,11 @@ struct Fetch {
     uint32_t hb[B_PER];
 };
 
-template <int FMT, int KB, int BM, int BN, int T>
+// Which part of a stage a fetch / store moves: both, the activations only or
+// the weights only.
+enum StagePart { kBoth = 0, kActs = 1, kWeights = 2 };
+
+template <int FMT, int KB, int BM, int BN, int T, int PART = kBoth>
 __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const Planes &P,
                                             const int8_t *__restrict__ xq, const float *__restrict__ xs,
                                             const int *__restrict__ sx, int m0, int n0, int M, int N, int G,
@@ -111,7 +115,7 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
 #pragma unroll
     for (int i = 0; i < F::A_PER; i++) {
         const int e = tid + T * i;
-        if (F::A_N % T == 0 || e < F::A_N) {
+        if (PART != kWeights && (F::A_N % T == 0 || e < F::A_N)) {
             const int m = min(m0 + e / KB, M - 1);  // rows past M reload the last row; never stored
             const v4i *p = (const v4i *)(xq + (size_t)m * K + (size_t)(g0 + e % KB) * 32);
             f.a[i][0] = p[0];
@@ -124,7 +128,7 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
 #pragma unroll
     for (int i = 0; i < F::B_PER; i++) {
         const int e = tid + T * i;
-        if (F::B_N % T == 0 || e < F::B_N) {
+        if (PART != kActs && (F::B_N % T == 0 || e < F::B_N)) {
             const int n = min(n0 + e / KB, N - 1);
             const size_t idx = (size_t)n * G + g0 + e % KB;
             f.b[i][0] = *(const v4i *)(P.qs + idx);
@@ -143,7 +147,7 @@ __device__ __forceinline__ bool f16_nonfinite(uint16_t h) { return (h & 0x7c00u)
 
 // Stores the fetched stage `stage` into LDS in the MFMA's element order; a
 // thread that sees a scale needing the exact epilogue writes `stage` to S.tag.
-template <int FMT, int KB, int BM, int BN, int T>
+template <int FMT, int KB, int BM, int BN, int T, int PART = kBoth>
 __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, Stage<FMT, KB, BM, BN> &S,
                                             int stage) {
     using F = Fetch<FMT, KB, BM, BN, T>;
@@ -153,7 +157,7 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
 #pragma unroll
     for (int i = 0; i < F::A_PER; i++) {
         const int e = tid + T * i;
-        if (F::A_N % T == 0 || e < F::A_N) {
+        if (PART != kWeights && (F::A_N % T == 0 || e < F::A_N)) {
             const int r = e / KB, blk = e % KB;
             v4i *p = (v4i *)(S.a + r * RB + blk * 32);
             p[0] = f.a[i][0];  // elements 0..15
@@ -166,7 +170,7 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
 #pragma unroll
     for (int i = 0; i < F::B_PER; i++) {
         const int e = tid + T * i;
-        if (F::B_N % T == 0 || e < F::B_N) {
+        if (PART != kActs && (F::B_N % T == 0 || e < F::B_N)) {
             const int r = e / KB, blk = e % KB;
             v4i *p = (v4i *)(S.b + r * RB + blk * 32);
             if (F::Q8) {
@@ -508,6 +512,42 @@ __global__ void __launch_bounds__(64 * WM * WN * WK) __attribute__((amdgpu_waves
             if (s + 1 < st1) fetch_stage<FMT, KB, BM, BN, T>(f, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * KB);
             compute(s);
             if (s + 1 < st1) store_stage<FMT, KB, BM, BN, T>(f, stages[(s + 1 - st0) & 1], s + 1);
+            __syncthreads();
+        }
+    } else if constexpr (FMT == SLLM_Q4_1) {
+        // The weights two stages ahead in two register sets filled alternately,
+        // the activations (mostly L2 hits) one stage ahead in a third. Each
+        // stage's activations are issued before the weights of the stage after
+        // it, so waiting for them leaves those weights in flight. Q4_1 only:
+        // with whole stages in both sets its 64 x 128 kernel spills, and the
+        // reloads wait for every load in flight (14336x4096 at M = 512 / 1024:
+        // 164-166 / 287-292 -> 160-161 / 277-280 us); Q8_0 and Q5K1 fit and
+        // gain nothing from it.
+        Fe fa, fb, xa;
+        auto put = [&](const Fe &w, int s) {
+            store_stage<FMT, KB, BM, BN, T, kActs>(xa, stages[(s - st0) & 1], s);
+            store_stage<FMT, KB, BM, BN, T, kWeights>(w, stages[(s - st0) & 1], s);
+        };
+        if (st0 < st1) {
+            fetch_stage<FMT, KB, BM, BN, T>(fa, P, xq, xs, sx, m0, n0, M, N, G, st0 * KB);
+            if (st0 + 1 < st1)
+                fetch_stage<FMT, KB, BM, BN, T, kWeights>(fb, P, xq, xs, sx, m0, n0, M, N, G, (st0 + 1) * KB);
+            store_stage<FMT, KB, BM, BN, T>(fa, stages[0], st0);
+        }
+        __syncthreads();
+        for (int s = st0; s < st1; s += 2) {
+            // stage s: fb holds the weights of stage s + 1
+            if (s + 1 < st1) fetch_stage<FMT, KB, BM, BN, T, kActs>(xa, P, xq, xs, sx, m0, n0, M, N, G, (s + 1) * KB);
+            if (s + 2 < st1) fetch_stage<FMT, KB, BM, BN, T, kWeights>(fa, P, xq, xs, sx, m0, n0, M, N, G, (s + 2) * KB);
+            compute(s);
+            if (s + 1 < st1) put(fb, s + 1);
+            __syncthreads();
+            if (s + 1 >= st1) break;
+            // stage s + 1: fa holds the weights of stage s + 2
+            if (s + 2 < st1) fetch_stage<FMT, KB, BM, BN, T, kActs>(xa, P, xq, xs, sx, m0, n0, M, N, G, (s + 2) * KB);
+            if (s + 3 < st1) fetch_stage<FMT, KB, BM, BN, T, kWeights>(fb, P, xq, xs, sx, m0, n0, M, N, G, (s + 3) * KB);
+            compute(s + 1);
+            if (s + 2 < st1) put(fa, s + 2);
             __syncthreads();
         }
     } else {
