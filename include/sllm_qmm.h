@@ -153,6 +153,19 @@ sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes);
 sllm_status sllm_weight_q6k_exact_blocks(const sllm_weight *w, int64_t *blocks);
 
 /*
+ * *yes = 1 when the prefill GEMM computes this Q5K1 weight with one int8 MFMA
+ * per block: every block's high-block scale is exactly 16 times its low scale
+ * (convertQ5KToTwoQ41, kquant_kernels.go:127-144, writes f16(16 d sc) and
+ * f16(d sc), so this holds unless 16 d sc overflows f16: d sc is a multiple of
+ * 2^-24, exact in f16 below its normal range), and the two halves' terms of a
+ * block are then one dot of
+ * the 5-bit codes scaled by the low scale. 0 otherwise and for every other
+ * format (the halves take one MFMA each). Decided at load. No counterpart in
+ * the reference.
+ */
+sllm_status sllm_weight_q5k1_one_mfma(const sllm_weight *w, int *yes);
+
+/*
  * Rebuild the reference Raw bytes (QuantWeight.Raw layout) from the device
  * planes into host memory (cap >= raw_bytes). Bit-exact inverse of the repack.
  * SLLM_Q2K / SLLM_Q3K: the GGUF super-block bytes the weight was made from.

@@ -19,6 +19,7 @@ struct sllm_weight {
     int layout = 0;  // the plane layout (SLLM_Q4K_STREAM: Q4_1 planes + the Q4_K headers;
                      // SLLM_Q6K_STREAM: Q8_0 planes + the streamed Q6_K planes)
     int64_t q6_exceptions = 0;  // SLLM_Q6K_STREAM: blocks the GEMV recomputes in fp64
+    bool q5_one_mfma = false;   // Q5K1 with dh = 16 d in every block: the GEMM's SLLM_Q5K1F form
     int groups = 0, rows = 0, cols = 0;
     int device = 0;
     void *base = nullptr;
@@ -482,13 +483,17 @@ int gemv_fmt(const sllm_weight *w) {
     return w->fmt;
 }
 
+// The GEMM kernel format of a weight: a Q5K1 weight whose high-block scales are
+// 16 times its low ones runs as one MFMA per block (SLLM_Q5K1F).
+int gemm_fmt(const sllm_weight *w) { return w->fmt == SLLM_Q5K1 && w->q5_one_mfma ? SLLM_Q5K1F : w->fmt; }
+
 // One weight's matmul on device buffers: the GEMV, or the GEMM with the given
 // activation workspace (at least gemm_workspace_bytes).
 sllm_status run_matmul(const sllm_weight *w, const float *x, int x_rows, float *dst, hipStream_t s, void *ws,
                        size_t cap) {
     const Planes P = as_const(w->planes);
     if (!uses_gemm(w, x_rows)) return launch_gemv(gemv_fmt(w), P, x, dst, w->rows, w->groups, x_rows, s);
-    return launch_gemm(w->fmt, P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
+    return launch_gemm(gemm_fmt(w), P, x, dst, w->rows, w->groups, x_rows, ws, cap, s);
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -498,7 +503,7 @@ size_t multi_gemm_ws(const sllm_weight *const *ws, int count, int x_rows) {
     size_t need = 0;
     for (int i = 0; i < count; i++)
         if (uses_gemm(ws[i], x_rows)) {
-            const size_t b = gemm_workspace_bytes(ws[i]->fmt, ws[i]->rows, ws[i]->groups, x_rows);
+            const size_t b = gemm_workspace_bytes(gemm_fmt(ws[i]), ws[i]->rows, ws[i]->groups, x_rows);
             need = b > need ? b : need;
         }
     return align256(need);
@@ -761,16 +766,20 @@ sllm_status sllm_weight_from_quant(const char *qtype, const void *raw, size_t ra
     if ((st = ensure_init()) != SLLM_OK) return st;
     sllm_weight *w = nullptr;
     if ((st = alloc_weight(fmt, rows, cols, &w)) != SLLM_OK) return st;
-    int flag = 0;
+    int flag[2] = {0, 0};  // malformed high half; a block with dh != 16 d
     st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
         int *err = (int *)((char *)c->buf + ((need + 255) & ~(size_t)255));
-        SLLM_HIP(hipMemsetAsync(err, 0, sizeof(int), c->stream));
+        SLLM_HIP(hipMemsetAsync(err, 0, 2 * sizeof(int), c->stream));
         sllm_status s2 = pack_from_raw(fmt, (const uint8_t *)c->buf, rows, groups, w->planes, err, c->stream);
         if (s2 != SLLM_OK) return s2;
-        SLLM_HIP(hipMemcpyAsync(&flag, err, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+        if (fmt == SLLM_Q5K1 &&
+            (s2 = check_q5k1_one_mfma(w->planes, (int64_t)rows * groups, err + 1, c->stream)) != SLLM_OK)
+            return s2;
+        SLLM_HIP(hipMemcpyAsync(flag, err, 2 * sizeof(int), hipMemcpyDeviceToHost, c->stream));
         return SLLM_OK;
     });
-    if (st == SLLM_OK && flag)
+    w->q5_one_mfma = fmt == SLLM_Q5K1 && flag[1] == 0;
+    if (st == SLLM_OK && flag[0])
         st = set_error(SLLM_ERR_FORMAT, "q5k1 high half is not in convertQ5KToTwoQ41 form (min 0, 0/1 nibbles)");
     if (st != SLLM_OK) {
         sllm_weight_destroy(w);
@@ -816,9 +825,19 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     sllm_weight *w = nullptr;
     if ((st = alloc_weight(fmt, rows, cols, &w, layout)) != SLLM_OK) return st;
     uint32_t q6stat[2] = {0, 0};
+    int q5bad = 1;
     st = with_upload(raw, need, 256, [&](Ctx *c) -> sllm_status {
         const uint8_t *dev = (const uint8_t *)c->buf;
         if (t == 8 || t == 2 || t == 3 || t == 6) return pack_from_raw(fmt, dev, rows, cols / 32, w->planes, nullptr, c->stream);
+        if (t == 13) {
+            int *bad = (int *)((char *)c->buf + ((need + 255) & ~(size_t)255));
+            SLLM_HIP(hipMemsetAsync(bad, 0, sizeof(int), c->stream));
+            sllm_status ps = pack_from_gguf(t, dev, rows, cols, w->planes, c->stream);
+            if (ps == SLLM_OK) ps = check_q5k1_one_mfma(w->planes, (int64_t)rows * (cols / 32), bad, c->stream);
+            if (ps != SLLM_OK) return ps;
+            SLLM_HIP(hipMemcpyAsync(&q5bad, bad, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+            return SLLM_OK;
+        }
         if (w->layout != SLLM_Q6K_STREAM) return pack_from_gguf(t, dev, rows, cols, w->planes, c->stream);
         SLLM_HIP(hipMemsetAsync(w->planes.q6stat, 0, sizeof(q6stat), c->stream));
         sllm_status ps = pack_q6k_stream(dev, rows, cols, w->planes, c->stream);
@@ -829,6 +848,7 @@ sllm_status sllm_weight_from_gguf(uint32_t t, const void *raw, size_t raw_bytes,
     if (st == SLLM_OK && q6stat[1] != 0)
         st = set_error(SLLM_ERR_DEVICE, "Q6_K stream pack: the fp64 requantization disagrees with the Q8_0 planes");
     w->q6_exceptions = q6stat[0];
+    w->q5_one_mfma = t == 13 && q5bad == 0;
     if (st != SLLM_OK) {
         sllm_weight_destroy(w);
         return st;
@@ -882,6 +902,12 @@ sllm_status sllm_weight_stream_bytes(const sllm_weight *w, size_t *bytes) {
 sllm_status sllm_weight_q6k_exact_blocks(const sllm_weight *w, int64_t *blocks) {
     if (!w || !blocks) return set_error(SLLM_ERR_ARG, "null pointer");
     *blocks = w->layout == SLLM_Q6K_STREAM ? w->q6_exceptions : -1;
+    return SLLM_OK;
+}
+
+sllm_status sllm_weight_q5k1_one_mfma(const sllm_weight *w, int *yes) {
+    if (!w || !yes) return set_error(SLLM_ERR_ARG, "null pointer");
+    *yes = gemm_fmt(w) == SLLM_Q5K1F ? 1 : 0;
     return SLLM_OK;
 }
 
@@ -949,7 +975,7 @@ sllm_status sllm_matmul_dev(const sllm_weight *w, const float *x, int x_rows, in
     hipStream_t s = (hipStream_t)stream;
     void *ws = nullptr;
     size_t cap = 0;
-    if (uses_gemm(w, x_rows) && (st = workspace(s, gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows), &ws,
+    if (uses_gemm(w, x_rows) && (st = workspace(s, gemm_workspace_bytes(gemm_fmt(w), w->rows, w->groups, x_rows), &ws,
                                                  &cap)) != SLLM_OK)
         return st;
     return run_matmul(w, x, x_rows, dst, s, ws, cap);
@@ -1256,7 +1282,7 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
     if (P.qh) P.qh += off;
     const int G = w->groups;
     const size_t xb = align256((size_t)x_rows * x_cols * 4);
-    const size_t gb = align256(gemm_workspace_bytes(w->fmt, n_rows, G, x_rows));
+    const size_t gb = align256(gemm_workspace_bytes(gemm_fmt(w), n_rows, G, x_rows));
     const size_t db = align256((size_t)x_rows * n_rows * 4);
     const size_t ob = (size_t)x_rows * n_rows * G * 4 * (w->fmt == SLLM_Q5K1 ? 2 : 1);
     Ctx *c = nullptr;
@@ -1264,7 +1290,7 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
     char *b = (char *)c->buf;
     hipError_t e = hipMemcpyAsync(b, x, (size_t)x_rows * x_cols * 4, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) {
-        st = launch_gemm_dots(w->fmt, P, (const float *)b, (float *)(b + xb + gb), n_rows, G, x_rows, b + xb, gb,
+        st = launch_gemm_dots(gemm_fmt(w), P, (const float *)b, (float *)(b + xb + gb), n_rows, G, x_rows, b + xb, gb,
                               (int32_t *)(b + xb + gb + db), c->stream);
         if (st == SLLM_OK) {
             e = hipMemcpyAsync(out, b + xb + gb + db, ob, hipMemcpyDeviceToHost, c->stream);
@@ -1290,13 +1316,13 @@ sllm_status sllm_matmul_add_dev(const sllm_weight *w, const float *x, int x_rows
     const Planes P = as_const(w->planes);
     if (!uses_gemm(w, x_rows)) return launch_gemv_add(gemv_fmt(w), P, x, dst, w->rows, w->groups, x_rows, s);
     // GEMM: the product into the workspace behind the GEMM's own, then dst += it
-    const size_t gb = align256(gemm_workspace_bytes(w->fmt, w->rows, w->groups, x_rows));
+    const size_t gb = align256(gemm_workspace_bytes(gemm_fmt(w), w->rows, w->groups, x_rows));
     const size_t n = (size_t)x_rows * w->rows;
     void *ws = nullptr;
     size_t cap = 0;
     if ((st = workspace(s, gb + n * sizeof(float), &ws, &cap)) != SLLM_OK) return st;
     float *tmp = (float *)((char *)ws + gb);
-    if ((st = launch_gemm(w->fmt, P, x, tmp, w->rows, w->groups, x_rows, ws, gb, s)) != SLLM_OK) return st;
+    if ((st = launch_gemm(gemm_fmt(w), P, x, tmp, w->rows, w->groups, x_rows, ws, gb, s)) != SLLM_OK) return st;
     return launch_add(dst, tmp, n, s);
 }
 

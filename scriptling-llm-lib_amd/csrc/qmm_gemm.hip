@@ -69,18 +69,28 @@ constexpr float kHugeXs = 0x1p90f;      // activation scales from here on take t
 
 __host__ __device__ constexpr int row_bytes(int KB) { return KB * 32 + 16; }  // padded: conflict-free b128 reads
 
+// Format traits. SLLM_Q5K1F is a Q5K1 weight with dh = 16 d in every block:
+// its codes are staged as q5 = nib + 16 bit, so one MFMA gives dot5 = dot +
+// 16 dot_h and dot5 * d = dot * d + dot_h * dh exactly; its dh plane is not
+// read (the exact path splits the codes back into the two halves and takes
+// 16 d for dh).
+__host__ __device__ constexpr bool has_min(int f) { return f == SLLM_Q4_1 || f == SLLM_Q5K1 || f == SLLM_Q5K1F; }
+__host__ __device__ constexpr bool two_mfma(int f) { return f == SLLM_Q5K1; }
+__host__ __device__ constexpr bool has_dh(int f) { return f == SLLM_Q5K1; }
+__host__ __device__ constexpr bool has_hb(int f) { return f == SLLM_Q5K1 || f == SLLM_Q5K1F; }
+
 template <int FMT, int KB, int BM, int BN>
 struct alignas(16) Stage {
-    static constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
-    static constexpr bool DUAL = FMT == SLLM_Q5K1;
+    static constexpr bool HAS_MIN = has_min(FMT);
+    static constexpr bool DUAL = two_mfma(FMT);
     int8_t a[BM * row_bytes(KB)];                          // activation codes
-    int8_t b[BN * row_bytes(KB)];  // weight codes (Q4_0: nib - 8, Q4_1 / Q5K1: nib, one per byte)
+    int8_t b[BN * row_bytes(KB)];  // weight codes (Q4_0: nib - 8, Q4_1 / Q5K1: nib, Q5K1F: nib + 16 bit)
     int8_t bh[(DUAL ? BN : 1) * row_bytes(KB)];            // Q5K1 high bits as 0 / 1 bytes
     float xs[KB][BM];                                      // activation scales
-    int aux[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? KB : 1][BM];  // float(Σxq) bits (exact, |Σxq| < 2^24)
+    int aux[HAS_MIN ? KB : 1][BM];                         // float(Σxq) bits (exact, |Σxq| < 2^24)
     float d[KB][BN];                                       // weight scales (Q8_0: the reference's f16 table)
     float m[HAS_MIN ? KB : 1][BN];                         // mins
-    float dh[DUAL ? KB : 1][BN];                           // Q5K1 high-block scales
+    float dh[has_dh(FMT) ? KB : 1][BN];                    // Q5K1 high-block scales
     int tag;  // the K stage index whose data needs the exact epilogue (any thread that sees it writes it)
 };
 
@@ -134,11 +144,9 @@ __device__ __forceinline__ void fetch_stage(Fetch<FMT, KB, BM, BN, T> &f, const 
             f.b[i][0] = *(const v4i *)(P.qs + idx);
             if (F::Q8) f.b[i][F::Q8 ? 1 : 0] = *(const v4i *)(P.qs2 + idx);
             f.d[i] = P.d[idx];
-            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) f.m[i] = P.m[idx];
-            if (FMT == SLLM_Q5K1) {
-                f.dh[i] = P.dh[idx];
-                f.hb[i] = P.qh[idx];
-            }
+            if (has_min(FMT)) f.m[i] = P.m[idx];
+            if (has_dh(FMT)) f.dh[i] = P.dh[idx];
+            if (has_hb(FMT)) f.hb[i] = P.qh[idx];
         }
     }
 }
@@ -163,7 +171,7 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
             p[0] = f.a[i][0];  // elements 0..15
             p[1] = f.a[i][1];  // elements 16..31
             S.xs[blk][r] = f.xs[i];
-            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) S.aux[blk][r] = __float_as_int((float)f.sx[i]);
+            if (has_min(FMT)) S.aux[blk][r] = __float_as_int((float)f.sx[i]);
             slow |= !(f.xs[i] < kHugeXs);
         }
     }
@@ -188,18 +196,27 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
 #pragma unroll
                     for (int k = 0; k < 8; k++) c[k] = ((c[k] | (int)0x80808080) - 0x08080808) ^ (int)0x80808080;
                 }
+                if (FMT == SLLM_Q5K1F) {
+                    // + 16 x the high bit; bits in group order: (hb >> k) & 0x01010101
+                    // are elements 4k .. 4k + 3, the elements of c[k]
+                    const int hb = (int)f.hb[i];
+#pragma unroll
+                    for (int k = 0; k < 8; k++) c[k] |= ((hb >> k) & 0x01010101) << 4;
+                }
                 p[0] = v4i{c[0], c[1], c[2], c[3]};
                 p[1] = v4i{c[4], c[5], c[6], c[7]};
             }
             S.d[blk][r] = (FMT == SLLM_Q8_0) ? f16_lut(f.d[i]) : f16_exact(f.d[i]);
             slow |= f16_nonfinite(f.d[i]);
-            if (FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) {
-                S.m[(FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1) ? blk : 0][r] = f16_exact(f.m[i]);
+            if (has_min(FMT)) {
+                S.m[has_min(FMT) ? blk : 0][r] = f16_exact(f.m[i]);
                 slow |= f16_nonfinite(f.m[i]);
             }
-            if (FMT == SLLM_Q5K1) {
-                S.dh[FMT == SLLM_Q5K1 ? blk : 0][r] = f16_exact(f.dh[i]);
+            if (has_dh(FMT)) {
+                S.dh[has_dh(FMT) ? blk : 0][r] = f16_exact(f.dh[i]);
                 slow |= f16_nonfinite(f.dh[i]);
+            }
+            if (FMT == SLLM_Q5K1) {
                 // high bits in group order: (hb >> k) & 0x01010101 = elements 4k .. 4k + 3
                 const int hb = (int)f.hb[i];
                 constexpr int m = 0x01010101;
@@ -216,8 +233,8 @@ __device__ __forceinline__ void store_stage(const Fetch<FMT, KB, BM, BN, T> &f, 
 // the MFMA operands and the scales the epilogue applies.
 template <int FMT, int CF>
 struct Ops {
-    static constexpr bool DUAL = FMT == SLLM_Q5K1;
-    static constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    static constexpr bool DUAL = two_mfma(FMT);
+    static constexpr bool HAS_MIN = has_min(FMT);
     v4i a;
     v4i b[CF], bh[DUAL ? CF : 1];
     float xv[16];                   // activation scales of the lane's 16 rows
@@ -273,7 +290,7 @@ struct MinOps {
 template <int FMT, int KB, int BM, int BN, int CF>
 __device__ __forceinline__ void load_min(MinOps<CF> &o, const Stage<FMT, KB, BM, BN> &S, int blkA, int blkB, int wm,
                                          int wn, int lane) {
-    constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    constexpr bool HAS_MIN = has_min(FMT);
     const int r32 = lane & 31, h = lane >> 5;
     const int blk = h ? blkB : blkA;
     const bool live = blk >= 0;
@@ -361,6 +378,25 @@ __device__ __forceinline__ void dots_piece(int j, const v16i &D, const v16i &Dh,
     }
 }
 
+// Debug: the block dots of column piece j as dots_piece writes them. Q5K1F:
+// the two halves' dots of the Q5K1 layout, from the MFMA the epilogue scales
+// (dot5 = dot + 16 dot_h) and one more of the high bits alone: dot = dot5 - 16
+// dot_h.
+template <int FMT, int CF>
+__device__ __forceinline__ void dbg_dots(const Ops<FMT, CF> &o, int j, const v16i &cmag, const v16i &D,
+                                         const v16i &Dh, int *dots, int m0, int n0, int wm, int wn, int lane, int M,
+                                         int N, int G, int g) {
+    if constexpr (FMT == SLLM_Q5K1F) {
+        const v16i H = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, (o.b[j] >> 4) & 0x01010101, cmag, 0, 0, 0);
+        v16i L;
+#pragma unroll
+        for (int v = 0; v < 16; v++) L[v] = D[v] - 16 * (H[v] - kMagicBits);
+        dots_piece<SLLM_Q5K1, CF>(j, L, H, dots, m0, n0, wm, wn, lane, M, N, G, g);
+    } else {
+        dots_piece<FMT, CF>(j, D, Dh, dots, m0, n0, wm, wn, lane, M, N, G, g);
+    }
+}
+
 // The NB blocks blk0, blk0 + WK, ... of one K stage for one wave, software-
 // pipelined: block i+1's LDS operands are read before block i's epilogue, and
 // its MFMA for piece j is issued as soon as block i's epilogue has consumed
@@ -371,7 +407,7 @@ template <int FMT, int KB, int BM, int BN, int CF, int NB, int WK, bool PIPE, bo
 __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int blk0, int wm, int wn, int lane,
                                            const v16i &cmag, v16f (&acc)[CF], int *dots,
                                            int m0, int n0, int M, int N, int G, int g0) {
-    constexpr bool HAS_MIN = FMT == SLLM_Q4_1 || FMT == SLLM_Q5K1;
+    constexpr bool HAS_MIN = has_min(FMT);
     auto min_pair = [&](int i, MinOps<CF> &mo) {
         load_min<FMT, KB, BM, BN, CF>(mo, S, blk0 + i * WK, i + 1 < NB ? blk0 + (i + 1) * WK : -1, wm, wn, lane);
     };
@@ -392,7 +428,7 @@ __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int 
             }
 #pragma unroll
             for (int j = 0; j < CF; j++) {
-                if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
+                if (DBG) dbg_dots<FMT, CF>(o, j, cmag, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
                 epilogue_piece<FMT, CF, false>(o, j, D[j], Dh[j], acc);
             }
         }
@@ -414,7 +450,7 @@ __device__ __forceinline__ void stage_fast(const Stage<FMT, KB, BM, BN> &S, int 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < CF; j++) {
-            if (DBG) dots_piece<FMT, CF>(j, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
+            if (DBG) dbg_dots<FMT, CF>(cur, j, cmag, D[j], Dh[j], dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
             epilogue_piece<FMT, CF, false>(cur, j, D[j], Dh[j], acc);
             // fence the MFMA between two epilogue pieces: left to itself the
             // scheduler sinks all of the next block's MFMAs below the last
@@ -434,14 +470,42 @@ __device__ __forceinline__ void stage_slow(const Stage<FMT, KB, BM, BN> &S, int 
                                            int N, int G, int g0) {
 #pragma unroll 1
     for (int i = 0; i < NB; i++) {
+        const int blk = blk0 + i * WK;
         Ops<FMT, CF> o;
-        load_ops<FMT, KB, BM, BN, CF, true>(o, S, blk0 + i * WK, wm, wn, lane);
+        load_ops<FMT, KB, BM, BN, CF, true>(o, S, blk, wm, wn, lane);
+        if constexpr (FMT == SLLM_Q5K1F) {
+            // the two halves apart, as Q5K1: low nibbles and high bits of the
+            // 5-bit codes, each half with its own scale
+            Ops<SLLM_Q5K1, CF> q;
+            q.a = o.a;
 #pragma unroll
-        for (int j = 0; j < CF; j++) {
-            v16i D, Dh;
-            mfma_piece<FMT, CF>(o, j, cmag, D, Dh);
-            if (DBG) dots_piece<FMT, CF>(j, D, Dh, dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk0 + i * WK);
-            epilogue_piece<FMT, CF, true>(o, j, D, Dh, acc);
+            for (int v = 0; v < 16; v++) {
+                q.xv[v] = o.xv[v];
+                q.av[v] = o.av[v];
+            }
+#pragma unroll
+            for (int j = 0; j < CF; j++) {
+                q.b[j] = o.b[j] & 0x0f0f0f0f;
+                q.bh[j] = (o.b[j] >> 4) & 0x01010101;
+                q.wd[j] = o.wd[j];
+                q.wm[j] = o.wm[j];
+                q.wdh[j] = 16.0f * o.wd[j];  // dh, exactly
+            }
+#pragma unroll
+            for (int j = 0; j < CF; j++) {
+                v16i D, Dh;
+                mfma_piece<SLLM_Q5K1, CF>(q, j, cmag, D, Dh);
+                if (DBG) dots_piece<SLLM_Q5K1, CF>(j, D, Dh, dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk);
+                epilogue_piece<SLLM_Q5K1, CF, true>(q, j, D, Dh, acc);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CF; j++) {
+                v16i D, Dh;
+                mfma_piece<FMT, CF>(o, j, cmag, D, Dh);
+                if (DBG) dots_piece<FMT, CF>(j, D, Dh, dots, m0, n0, wm, wn, lane, M, N, G, g0 + blk);
+                epilogue_piece<FMT, CF, true>(o, j, D, Dh, acc);
+            }
         }
     }
 }
@@ -940,8 +1004,16 @@ GemmPlan plan_gemm(int fmt, int M, int N, int G) {
     // 180; Q5K1 14336x4096 kDeepS 52 / 85 / 276, kDeep 54 / 84 / 306, wide
     // 100 / 168 / 575 (its wide tiles spill).
     // (Q5K1 with up to 32 activation rows: 32-row tiles; Q5K1 4096x4096 at M
-    // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.)
-    p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : (M > 128 ? kWide2 : kWide);
+    // = 32 19.1 us against 23.2 at M = 33 on 64-row ones.) Q5K1F (one MFMA
+    // per block): 32-row tiles up to 32 rows, 64 x 64 up to 128, then 64 x
+    // 128 with one stage in flight (its two-stage kernel spills). Measured
+    // (us, kDeepS32 / kDeep / kWide): 14336x4096 at M = 16 28.7 / 31.5 / 30.3,
+    // M = 64 44.0 / 35.8 / 35.9, M = 512 264.9 / 187.4 / 175.4 (kWide2 208);
+    // 4096x4096 at M = 64 21.3 / 21.0 / 25.4, M = 512 85.3 / 61.8 / 60.0.
+    if (fmt == SLLM_Q5K1F)
+        p.shape = M <= 32 ? kDeepS32 : (M <= 128 ? kDeep : kWide);
+    else
+        p.shape = fmt == SLLM_Q5K1 ? (M <= 32 ? kDeepS32 : kDeepS) : (M > 128 ? kWide2 : kWide);
     if (tuning().gemm_shape >= 1 && tuning().gemm_shape <= 5) p.shape = tuning().gemm_shape - 1;
     p.bm = shape_bm(p.shape);
     p.bn = shape_bn(p.shape);
@@ -993,6 +1065,7 @@ sllm_status launch_int8(int fmt, const Planes &P, const int8_t *xq, const float 
     case SLLM_Q4_0: return launch_fmt<SLLM_Q4_0, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     case SLLM_Q4_1: return launch_fmt<SLLM_Q4_1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     case SLLM_Q5K1: return launch_fmt<SLLM_Q5K1, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
+    case SLLM_Q5K1F: return launch_fmt<SLLM_Q5K1F, DBG>(P, xq, xsp, sxp, out, M, N, G, p, dots, s);
     }
     return set_error(SLLM_ERR_QTYPE, "gemm: format has no int8 MFMA path");
 }

@@ -78,6 +78,12 @@ constexpr int SLLM_Q4K_STREAM = 7;
 // Internal only: such a weight is a "q8" QuantWeight at the ABI, and its Q8_0
 // planes, kept beside the stream's, serve the GEMM and the export.
 constexpr int SLLM_Q6K_STREAM = 8;
+// GEMM format of a Q5K1 weight whose high-block scale is 16 times its low
+// scale in every block (as convertQ5KToTwoQ41 writes them unless 16 d sc
+// overflows f16): its codes are staged as the 5-bit q5 = nib + 16 *
+// bit, one MFMA per block, whose dot scaled by the low scale is the two halves'
+// terms together. Internal only (the weight is a "q5k1" QuantWeight).
+constexpr int SLLM_Q5K1F = 9;
 
 // Formats whose activations stay fp32 (no Q8_0 codes): Q5_0 and the native k-quants.
 __host__ __device__ constexpr bool act_f32(int fmt) {
@@ -223,6 +229,9 @@ sllm_status pack_from_f32(const float *w_dev, int rows, int cols, const MutPlane
 // GGUF Q6_K -> the Q8_0 planes and the streamed Q6_K planes (P.q6stat zeroed
 // by the caller; the pack counts into it).
 sllm_status pack_q6k_stream(const uint8_t *raw_dev, int rows, int cols, const MutPlanes &P, hipStream_t s);
+// *bad_dev (cleared by the caller) set unless every block of a Q5K1 weight's
+// planes has dh = 16 d: the condition for the GEMM's one-MFMA form.
+sllm_status check_q5k1_one_mfma(const MutPlanes &P, int64_t nb, int *bad_dev, hipStream_t s);
 // GGUF super-block bytes of a native k-quant weight from its (host copy of the) planes.
 void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *out);
 

@@ -216,6 +216,18 @@ __global__ void pack_q5k_kernel(const uint8_t *__restrict__ raw, int64_t nb, Mut
     }
 }
 
+// The GEMM's one-MFMA form of a Q5K1 weight (SLLM_Q5K1F) needs every block's
+// high-block scale to equal 16 times its low scale. convertQ5KToTwoQ41 writes
+// f16(16 d sc) and f16(d sc) (kquant_kernels.go:127-144): equal to 16 times
+// the latter unless 16 d sc overflows f16 (d sc is a multiple of 2^-24, exact
+// in f16 below its normal range); a "q5k1" QuantWeight may hold any scales. *bad (cleared by the caller) is
+// set when some block differs (a NaN never equals).
+__global__ void q5k1_scale_check_kernel(const uint16_t *__restrict__ d, const uint16_t *__restrict__ dh, int64_t nb,
+                                        int *bad) {
+    for (int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; b < nb; b += (int64_t)gridDim.x * blockDim.x)
+        if (!(f16_exact(dh[b]) == 16.0f * f16_exact(d[b]))) *bad = 1;
+}
+
 // Q6_K (210 B / 256) -> Q8_0 planes. Q8 block b of a super-block covers
 // elements 32*(b%8) ..: half n = (b%8)/4, quarter k = (b%8)%4 of dequantizeQ6KBlock.
 __global__ void pack_q6k_kernel(const uint8_t *__restrict__ raw, int64_t nb, MutPlanes P) {
@@ -495,6 +507,12 @@ void export_kq_native(int fmt, const MutPlanes &p, int64_t nb, uint8_t *o) {
             sb[109] = (uint8_t)((p.sb[s] >> 8) & 0xff);
         }
     }
+}
+
+sllm_status check_q5k1_one_mfma(const MutPlanes &P, int64_t nb, int *bad_dev, hipStream_t s) {
+    hipLaunchKernelGGL(q5k1_scale_check_kernel, dim3(grid_for(nb)), dim3(256), 0, s, P.d, P.dh, nb, bad_dev);
+    SLLM_HIP(hipGetLastError());
+    return SLLM_OK;
 }
 
 sllm_status pack_q6k_stream(const uint8_t *raw_dev, int rows, int cols, const MutPlanes &P, hipStream_t s) {

@@ -106,6 +106,7 @@ def lib() -> C.CDLL:
     L.sllm_matmul_add_dev.argtypes = [W, P, i32, i32, P, P]
     L.sllm_weight_stream_bytes.argtypes = [W, C.POINTER(sz)]
     L.sllm_weight_q6k_exact_blocks.argtypes = [W, C.POINTER(C.c_int64)]
+    L.sllm_weight_q5k1_one_mfma.argtypes = [W, C.POINTER(i32)]
     L.sllm_kv_cache_create.argtypes = [i32, i32, i32, i32, C.POINTER(P)]
     L.sllm_kv_cache_destroy.argtypes = [P]
     L.sllm_kv_cache_length.argtypes = [P, i32, C.POINTER(i32)]
@@ -211,6 +212,14 @@ class DeviceWeight:
         n = C.c_int64()
         _check(lib().sllm_weight_q6k_exact_blocks(self.handle, C.byref(n)))
         return n.value
+
+    @property
+    def q5k1_one_mfma(self) -> bool:
+        """Q5K1: the prefill GEMM takes one MFMA per block (every block's
+        high-block scale is 16 x its low scale; sllm_weight_q5k1_one_mfma)."""
+        n = C.c_int()
+        _check(lib().sllm_weight_q5k1_one_mfma(self.handle, C.byref(n)))
+        return bool(n.value)
 
     @classmethod
     def from_quant(cls, w: QuantWeight) -> "DeviceWeight":

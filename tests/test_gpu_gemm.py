@@ -222,3 +222,102 @@ def test_gemm_rows_match_gemv_rows_q5(qtype):
         one = sq.model_matmul_row_quant_into_f32(w, x[row])
         bound = term_abs_sum(qtype, raw, N, x[row:row + 1])[0]
         assert np.all(np.abs(big.reshape(70, N)[row].astype(np.float64) - one) <= 2e-5 * bound + 1e-30), row
+
+
+def _q5k1_split_scales(raw: np.ndarray, N: int, K: int, blocks) -> np.ndarray:
+    """The q5k1 Raw with the given high blocks' scales moved off 16 x the low
+    scale (x 1.5), so the weight keeps one MFMA per half."""
+    G = K // 32
+    out = raw.copy()
+    lo = out[: N * G * 20].reshape(N * G, 20)
+    hi = out[N * G * 20:].reshape(N * G, 20)
+    for b in blocks:
+        d = lo[b, 0:2].view(np.float16)[0]
+        hi[b, 0:2] = np.array([np.float16(np.float32(d) * 24.0)]).view(np.uint8)
+    return out
+
+
+def test_q5k1_one_mfma_decided_at_load():
+    # dh = 16 d in every block (as convertQ5KToTwoQ41 writes it for d sc in the
+    # f16 normal range): one MFMA per block; otherwise one per half
+    N, K = 64, 512
+    raw = make_raw("q5k1", N, K, seed=3)
+    assert sq.DeviceWeight.from_quant(sq.QuantWeight("q5k1", raw, K // 32, N, K)).q5k1_one_mfma
+    split = _q5k1_split_scales(raw, N, K, [5])
+    assert not sq.DeviceWeight.from_quant(sq.QuantWeight("q5k1", split, K // 32, N, K)).q5k1_one_mfma
+    w = sq.load_weight_f32_direct(synth.GGML_Q5_K, synth.q5k_blocks(4, N, K), N, K)
+    assert w.q5k1_one_mfma
+    # a super-block whose 16 d sc overflows f16 (d = 100, sub-block 0's sc =
+    # 63): its high block's scale is Inf, not 16 x the low one
+    gg = synth.q5k_blocks(5, N, K).reshape(-1, 176).copy()
+    gg[7, 0:2] = np.array([np.float16(100.0)]).view(np.uint8)
+    gg[7, 4] = (gg[7, 4] & 0xC0) | 63
+    w2 = sq.load_weight_f32_direct(synth.GGML_Q5_K, gg.reshape(-1), N, K)
+    ex = w2.export()
+    G = K // 32
+    lo = ex[: N * G * 20].reshape(N * G, 20)[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    hi = ex[N * G * 20:].reshape(N * G, 20)[:, 0:2].copy().view(np.float16).astype(np.float32).ravel()
+    assert w2.q5k1_one_mfma == bool(np.all(hi == 16 * lo))
+    assert not w2.q5k1_one_mfma
+    assert not sq.load_weight_f32_direct(synth.GGML_Q4_K, synth.q4k_blocks(6, N, K), N, K).q5k1_one_mfma
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("M", [16, 64, 130, 300])
+def test_q5k1_one_and_two_mfma_forms(split, M):
+    # both GEMM forms of a Q5K1 weight against the oracle (the two halves'
+    # passes, kquant_kernels.go:159-174), on every workgroup shape
+    N, K = 192, 1024
+    raw = make_raw("q5k1", N, K, seed=M)
+    if split:
+        raw = _q5k1_split_scales(raw, N, K, [0, 77, N * (K // 32) - 1])
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight("q5k1", raw, K // 32, N, K))
+    assert w.q5k1_one_mfma == (not split)
+    x = make_x(M, K, seed=M + 1)
+    ref = oracle.matmul("q5k1", raw, N, x)
+    bound = term_abs_sum("q5k1", raw, N, x)
+    for shape in (0, 1, 2, 3, 4, 5):
+        sq.set_param("gemm_shape", shape)
+        try:
+            got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+        finally:
+            sq.set_param("gemm_shape", 0)
+        assert_fp32_parity(got.reshape(M, N), ref, bound, f"q5k1 split={split} M={M} shape={shape}")
+
+
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("shape", [1, 3, 4, 5])
+def test_q5k1_block_dots_both_forms(split, shape):
+    # the one-MFMA form's dots (dot + 16 dot_h, split back with one more MFMA
+    # of the high bits) and the two-MFMA form's, bit for bit
+    N, K, M = 200, 1024, 72
+    raw = make_raw("q5k1", N, K, seed=shape + 40)
+    if split:
+        raw = _q5k1_split_scales(raw, N, K, [3])
+    x = make_x(M, K, seed=shape)
+    x[1] = 0.0
+    x[2, :64] = np.float32(1e30)
+    _block_dots_case("q5k1", raw, N, K, x, 0, N, shape)
+    _block_dots_case("q5k1", raw, N, K, x, 37, 101, shape)
+
+
+@pytest.mark.parametrize("scale", ["inf", "nan"])
+def test_q5k1_one_mfma_nonfinite_scale(scale):
+    # a non-finite low scale with dh = 16 d (inf) keeps the one-MFMA form and
+    # takes the exact path for that stage; NaN never equals, so that weight
+    # keeps two MFMAs: both give the oracle's result
+    N, K, M = 96, 512, 64
+    G = K // 32
+    raw = make_raw("q5k1", N, K, seed=9).copy()
+    lo = raw[: N * G * 20].reshape(N * G, 20)
+    hi = raw[N * G * 20:].reshape(N * G, 20)
+    v = np.float16(np.inf) if scale == "inf" else np.float16(np.nan)
+    lo[10, 0:2] = np.array([v]).view(np.uint8)
+    hi[10, 0:2] = np.array([v]).view(np.uint8)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight("q5k1", raw, G, N, K))
+    assert w.q5k1_one_mfma == (scale == "inf")
+    x = make_x(M, K, seed=10)
+    got, _, _ = sq.model_matmul_quant_into_f32(w, x, M, K)
+    ref = oracle.matmul("q5k1", raw, N, x)
+    assert not np.isfinite(ref).all()
+    assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum("q5k1", raw, N, x), f"q5k1 {scale}")
