@@ -55,8 +55,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 __device__ void prep_row(float *row, const float *src, int dk, const float *bias, int j0, int blen,
                          const float *nw, float eps, const float *freqs, int half, int pos, int lane) {
-    // this lane's first rotation frequency, loaded with the row (half <= 64 in one pass)
+    // this lane's first rotation frequency and its norm weights (d = lane +
+    // 64 j, dk <= 256), loaded with the row: one memory round trip in all
     const float f0 = lane < half ? freqs[lane] : 0.0f;
+    float wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) wv[j] = nw && lane + 64 * j < dk ? nw[lane + 64 * j] : 0.0f;
     for (int d = lane; d < dk; d += 64) {
         float x = src[d];
         if (bias && j0 + d < blen) x = x + bias[j0 + d];
@@ -74,7 +78,11 @@ __device__ void prep_row(float *row, const float *src, int dk, const float *bias
         const float ss = ((w[0] + w[1]) + w[2]) + w[3];
         const float inv = 1.0f / (float)sqrt((double)ss / (double)dk + (double)eps);
         wave_lds_sync();
-        for (int d = lane; d < dk; d += 64) row[d] = (row[d] * inv) * nw[d];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = lane + 64 * j;
+            if (d < dk) row[d] = (row[d] * inv) * wv[j];
+        }
         wave_lds_sync();
     }
     for (int i = lane; i < half; i += 64) {
@@ -231,19 +239,36 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
             prep_row(qs + hr * dk, a.q + (size_t)qi * a.n_heads * dk + (size_t)h * dk, dk, a.q_bias, h * dk, a.qb_len,
                      a.q_norm, a.eps, a.freqs, a.half_dim, pos, lane);
         }
-        // the workgroup's last wave; every head slice builds the row for itself,
-        // slice 0 appends it to the cache
-        if (owns_new && wave == (int)(blockDim.x >> 6) - 1) {
+        // the first wave of group 0 that prepares no q head (waves 0 .. nh - 1
+        // start first; with every group-0 wave on a q head, the workgroup's
+        // last wave); every head slice builds the row for itself, slice 0
+        // appends it to the cache
+        const int kwave = hp < nh ? hp : (int)(blockDim.x >> 6) - 1;
+        if (owns_new && wave == kwave) {
             const size_t off = (size_t)qi * a.n_kv * dk + (size_t)g * dk;
+            // the v row (d = lane + 64 j, dk <= 256) is loaded before the k
+            // row is prepared, so its memory round trip overlaps that work
+            float vv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = lane + 64 * j;
+                vv[j] = 0.0f;
+                if (d < dk) {
+                    vv[j] = a.v[off + d];
+                    if (a.v_bias && g * dk + d < a.vb_len) vv[j] = vv[j] + a.v_bias[g * dk + d];
+                }
+            }
             prep_row(nk, a.k + off, dk, a.k_bias, g * dk, a.kb_len, a.k_norm, a.eps, a.freqs, a.half_dim, pos, lane);
             const size_t at = ((size_t)g * a.cap + (size_t)a.cache_len) * dk;
-            for (int d = lane; d < dk; d += 64) {
-                float x = a.v[off + d];
-                if (a.v_bias && g * dk + d < a.vb_len) x = x + a.v_bias[g * dk + d];
-                nk[dk + d] = x;
-                if (sl == 0) {
-                    a.cache_k[at + d] = nk[d];
-                    a.cache_v[at + d] = x;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = lane + 64 * j;
+                if (d < dk) {
+                    nk[dk + d] = vv[j];
+                    if (sl == 0) {
+                        a.cache_k[at + d] = nk[d];
+                        a.cache_v[at + d] = vv[j];
+                    }
                 }
             }
         }
@@ -301,7 +326,10 @@ __global__ void __launch_bounds__(kMaxWaves * 64) attn_split_kernel(AttnArgs a) 
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
             const float mn = fmaxf(m, mt);
-            const float alpha = (float)exp((double)(m - mn));
+            // a group's first tile (running max still -inf) against a finite
+            // max: exp(-inf) = 0 exactly, without the fp64 exp on the chain
+            const float alpha = (m == -INFINITY && mn > -INFINITY && mn < INFINITY) ? 0.0f
+                                                                                  : (float)exp((double)(m - mn));
             e = lane < n ? (float)exp((double)(sc - mn)) : 0.0f;
             l = l * alpha + wave_sum(e);
             m = mn;
