@@ -935,12 +935,27 @@ __global__ void __launch_bounds__(128 * WN) gemm_q5_kernel(Planes P, const uint1
     }
 }
 
-// dst = part[0] + part[1] + ... + part[S-1], in split order.
+// dst = part[0] + part[1] + ... + part[S-1], added in split order. V floats
+// per thread (V = 4: float4 loads and stores, n a multiple of 4 and dst 16-byte
+// aligned); the loads of up to eight splits are issued before their adds (a
+// load-add chain waited for every split's load in turn).
+template <int V>
 __global__ void reduce_splits_kernel(const float *__restrict__ part, float *__restrict__ dst, size_t n, int S) {
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
-        float v = part[i];
-        for (int s = 1; s < S; s++) v = v + part[(size_t)s * n + i];
-        dst[i] = v;
+    typedef float vec __attribute__((ext_vector_type(V)));
+    const size_t nv = n / V;
+    const vec *pv = (const vec *)part;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < nv; i += (size_t)gridDim.x * blockDim.x) {
+        vec v = pv[i];
+        for (int s0 = 1; s0 < S; s0 += 8) {
+            vec p[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (s0 + k < S) p[k] = pv[(size_t)(s0 + k) * nv + i];
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (s0 + k < S) v = v + p[k];
+        }
+        ((vec *)dst)[i] = v;
     }
 }
 
@@ -1112,9 +1127,13 @@ sllm_status gemm_impl(int fmt, const Planes &P, const float *x, float *dst, int 
     }
     if (st != SLLM_OK || p.splits == 1) return st;
     const size_t n = (size_t)M * N;
-    int grid = (int)((n + 255) / 256);
+    const bool v4 = n % 4 == 0 && ((uintptr_t)dst & 15) == 0;
+    int grid = (int)((n / (v4 ? 4 : 1) + 255) / 256);
     if (grid > 4096) grid = 4096;
-    hipLaunchKernelGGL(reduce_splits_kernel, dim3(grid), dim3(256), 0, s, part, dst, n, p.splits);
+    if (v4)
+        hipLaunchKernelGGL(reduce_splits_kernel<4>, dim3(grid), dim3(256), 0, s, part, dst, n, p.splits);
+    else
+        hipLaunchKernelGGL(reduce_splits_kernel<1>, dim3(grid), dim3(256), 0, s, part, dst, n, p.splits);
     SLLM_HIP(hipGetLastError());
     return SLLM_OK;
 }

@@ -66,6 +66,38 @@ def test_shape_and_split_overrides(qtype, shape, splits):
     assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} shape={shape} S={splits}")
 
 
+@pytest.mark.parametrize("splits", [9, 12, 16])
+@pytest.mark.parametrize("N,M", [(256, 64), (255, 65)])
+def test_split_reduction_layouts(splits, N, M):
+    # the split reduction adds the partial tiles in split order whether it
+    # moves four floats per thread (element count a multiple of 4, output
+    # 16-byte aligned) or one (odd count, or an output 4 bytes off alignment),
+    # with more splits than it loads at once: every layout gives the same bits,
+    # within the bound of the oracle's result
+    import torch
+
+    qtype, K = "q8", 4096
+    raw = make_raw(qtype, N, K, seed=splits + N)
+    x = make_x(M, K, seed=splits)
+    w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
+    torch.cuda.set_device(0)
+    s = torch.cuda.current_stream()
+    xd = torch.from_numpy(x).cuda()
+    buf = torch.zeros(M * N + 8, device="cuda")
+    outs = []
+    sq.set_param("gemm_splits", splits)
+    try:
+        for off in (0, 1):
+            sq.matmul_dev(w, xd.data_ptr(), M, K, buf.data_ptr() + 4 * off, s.cuda_stream)
+            torch.cuda.synchronize()
+            outs.append(buf[off:off + M * N].cpu().numpy().copy())
+    finally:
+        sq.set_param("gemm_splits", 0)
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    ref = oracle.matmul(qtype, raw, N, x)
+    assert_fp32_parity(outs[0].reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"S={splits} {N}x{K} M={M}")
+
+
 def _block_dots_case(qtype, raw, N, K, x, row0, n_rows, shape=0):
     w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
     sq.set_param("gemm_shape", shape)
