@@ -447,7 +447,9 @@ sllm_status sllm_debug_gemm_block_dots(const sllm_weight *w, const float *x, int
  *                                  stages of loads in flight, 4 = 32 x 64 tiles with each
  *                                  stage split over four waves, 5 = as 1 with two stages of
  *                                  loads in flight (0: 1, above 128 rows 5; for Q5K1 3,
- *                                  and 4 up to 32 rows); Q5_0: 1 = 64 x 256
+ *                                  and 4 up to 32 rows; for Q5K1 in one MFMA per block,
+ *                                  see sllm_weight_q5k1_one_mfma, 4 up to 32 rows, 2 up
+ *                                  to 128, else 1); Q5_0: 1 = 64 x 256
  *                                  tiles, 2 = 64 x 128 (0: 2 up to 4096 weight rows and
  *                                  128 activation rows, else 1). The shape moves the fp32
  *                                  summation splits
