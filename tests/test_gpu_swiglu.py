@@ -57,6 +57,31 @@ def test_swiglu_fused(fmt_g, fmt_u, M):
     assert np.all(np.abs(h.cpu().numpy().astype(np.float64) - href) <= bound)
 
 
+@pytest.mark.parametrize("N", [1, 7, 2500, 4500, 4501])
+@pytest.mark.parametrize("M", [1, 2, 3])
+def test_swiglu_row_counts(N, M):
+    # paired launches over row counts that give one, two or more rows per wave
+    # with strided and consecutive rows, spare waves and a short last wave
+    # (4501): each row sum is formed as the single matmul forms it, so the
+    # outputs are bit for bit those of the single matmuls and the oracle's
+    # SwiGLU of them.
+    K = 1024
+    _, wg = _w("q4_1", N, K, seed=N + M)
+    _, wu = _w("q4_1", N, K, seed=N + M + 1)
+    x = make_x(M, K, seed=N)
+    xd = torch.from_numpy(x).cuda()
+    h, gt, up, g1, u1 = (torch.empty(M * N, device="cuda") for _ in range(5))
+    s = torch.cuda.current_stream().cuda_stream
+    sq.matmul_swiglu_dev(wg, wu, xd.data_ptr(), M, K, h.data_ptr(), gt.data_ptr(), up.data_ptr(), s)
+    sq.matmul_dev(wg, xd.data_ptr(), M, K, g1.data_ptr(), s)
+    sq.matmul_dev(wu, xd.data_ptr(), M, K, u1.data_ptr(), s)
+    torch.cuda.synchronize()
+    assert torch.equal(gt.view(torch.int32), g1.view(torch.int32))
+    assert torch.equal(up.view(torch.int32), u1.view(torch.int32))
+    want = oracle.swiglu(gt.cpu().numpy(), up.cpu().numpy())
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_swiglu_host_entry_equals_device():
     N, K, M = 256, 1024, 2
     _, wg = _w("q4_1", N, K, seed=1)
