@@ -162,10 +162,15 @@ __device__ __forceinline__ void quantize_part(const float4 *v, int *w, float &sc
 // s = float32(1.0 / (1.0 + exp(-float64(gate)))) in fp64, then (gate * s) * up
 // in fp32. exp is the device's fp64 exp (faithfully rounded), where the
 // reference calls Go's math.Exp.
-__device__ __forceinline__ float swiglu(float gate, float up) {
+// swiglu_gate is the part that depends on gate alone: swiglu(g, u) is
+// swiglu_gate(g) * u, operation for operation.
+__device__ __forceinline__ float swiglu_gate(float gate) {
     const double e = exp(-(double)gate);
     const float s = (float)(1.0 / (1.0 + e));
-    const float t = gate * s;
+    return gate * s;
+}
+__device__ __forceinline__ float swiglu(float gate, float up) {
+    const float t = swiglu_gate(gate);
     return t * up;
 }
 

@@ -99,8 +99,16 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         return w;
     };
     while (count_waves(RPW) > slots) RPW++;
+    // Paired gate / up: half of a workgroup's waves stream gate rows, the other
+    // half the same rows of up, RPW consecutive rows per wave, so both weights
+    // stream as one unpaired launch over the 2N rows would; the workgroup's
+    // gate and up waves then meet in LDS.
+    if (pair) {
+        RPW = (int)((2 * (int64_t)N[0] + slots - 1) / slots);
+        while (2 * (((int64_t)N[0] + RPW - 1) / RPW) > slots) RPW++;
+    }
     if (RPW > 64) return set_error(SLLM_ERR_SHAPE, "gemv: more than 64 rows per wave (rows too many)");
-    const int64_t waves = count_waves(RPW);
+    const int64_t waves = pair ? 2 * (((int64_t)N[0] + RPW - 1) / RPW) : count_waves(RPW);
     // Blocks per lane per unit (NB) and K-chunks per row (KCH). Rows of up to
     // gemv_max_nb x 64 blocks are one chunk; longer rows are split into chunks
     // of the largest lane-group count that divides them (no partial chunks).
@@ -121,8 +129,7 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
         while (NB > 1 && lg % NB) NB--;
         if (NB * 2 < nb_cap) NB = nb_cap;  // no good divisor: accept one partial chunk
     }
-    const int passes = pair ? 2 : 1;
-    while (NB > 1 && RPW * passes * ((lg + NB - 1) / NB) < 4) {
+    while (NB > 1 && RPW * ((lg + NB - 1) / NB) < 4) {
         int nb = NB - 1;
         while (nb > 1 && lg % nb) nb--;
         NB = nb;
@@ -130,7 +137,9 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     const int KCH = (G + 64 * NB - 1) / (64 * NB);
     int W = (int)((waves + wgs - 1) / wgs);
     W = W < 4 ? 4 : (W > T.gemv_waves ? T.gemv_waves : W);
-    const int grid = (int)((waves + W - 1) / W);
+    if (pair) W = (W + 1) & ~1;  // as many gate waves as up waves (gemv_waves is even)
+    const int grid = pair ? (int)(((int64_t)N[0] + (int64_t)(W / 2) * RPW - 1) / ((int64_t)(W / 2) * RPW))
+                          : (int)((waves + W - 1) / W);
     if (amax_key && (M != 1 || nseg != 1 || pair)) return set_error(SLLM_ERR_ARG, "gemv: argmax needs one row");
     if (norm_w && M != 1) return set_error(SLLM_ERR_ARG, "gemv: the fused RMSNorm takes one activation row");
     SegTable S{};
@@ -148,7 +157,7 @@ sllm_status plan_and_launch(int fmt, const Planes *P, float *const *dst, const i
     }
     for (int i = 0; i < nrow_segs; i++) S.wave0[i + 1] = S.wave0[i] + (N[i] + RPW - 1) / RPW;
     S.wave0[nrow_segs] = grid * W;  // the last segment also takes the spare waves
-    const int U = RPW * KCH * passes;
+    const int U = RPW * KCH;
     int done = 0;
     while (done < M) {
         const int left = M - done;

@@ -564,8 +564,10 @@ __device__ __forceinline__ void argmax_tail(const SegTable &S, float v, bool min
 // (at most RPW of them; consecutive rows for an odd RPW, rows strided by the
 // segment's wave count otherwise). A unit is NB blocks per lane. The wave keeps D units in
 // flight in a register ring: it computes unit t, then issues the loads of
-// unit t + D into the registers it just consumed. PAIR: each row is streamed
-// twice, gate chunks then up chunks, and the wave combines the two sums.
+// unit t + D into the registers it just consumed. PAIR: the first half of a
+// workgroup's waves stream gate rows, the second half the same rows of up
+// (each wave RPW consecutive rows of one weight, as an unpaired launch
+// streams them), and the two sums of a row meet in LDS for the SwiGLU.
 // NORM: the activation row (M == 1) is RMSNormed (S.norm_w, S.norm_eps) on the way in.
 template <int FMT, int NB, int D, int MT, bool HOIST, bool PAIR, bool NORM>
 __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__restrict__ x, int G, int M,
@@ -591,11 +593,13 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     }
     const Planes P2 = S.P[PAIR ? 1 : 0];  // PAIR: the up planes
     const int wv = wg - w0;
-    constexpr int PH = PAIR ? 2 : 1;  // passes over each row
-    const int U = RPW * KCH * PH;
+    // PAIR: this wave's half of the workgroup (gate or up) and its place in it
+    const int H = W >> 1, wi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool upw = PAIR && wi >= H;
+    const int U = RPW * KCH;
     constexpr int CH = 64 * NB;  // blocks per K-chunk
 
-    // Load-stream position (row ordinal lq, chunk lk, pass lp; lt units issued). Every
+    // Load-stream position (row ordinal lq, chunk lk; lt units issued). Every
     // wave runs U units; one with fewer than RPW rows re-reads its last real
     // unit for the rest (the data is still in flight or in cache, and no two
     // waves pile onto the same lines); those rows' sums land in lanes >=
@@ -605,32 +609,30 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     // even one the rows wv, wv + TW, ... strided by the segment's wave count.
     // Measured (same box, bit-identical): the fused C3 gate+up (RPW 7) 13.24
     // against 13.55-13.65 µs with strided rows; the RMSNorm + head + argmax
-    // (RPW 32) 87.0-87.7 strided against 90.8-91.3 consecutive and RMSNorm +
-    // gate/up + SwiGLU (4 pairs) 15.07-15.11 against 15.31-15.38: with an even
+    // (RPW 32) 87.0-87.7 strided against 90.8-91.3 consecutive: with an even
     // RPW the waves' stretches start a power-of-two multiple of the 2 KB plane
     // rows apart, and their concurrent loads share HBM channels.
+    // PAIR: rows blockIdx.x * H * RPW + (wi % H) * RPW, ... (RPW consecutive;
+    // C3: 7 on 16 waves per CU, as the unpaired gate + up). Against each wave
+    // streaming 4 rows' gate and up halves in turn on 14 waves per CU (rows
+    // strided): RMSNorm + gate/up + SwiGLU 15.00 -> 14.57 µs, without the
+    // norm 14.38 -> 13.87.
     const int TW = w1 - w0;
-    const bool consec = (RPW & 1) != 0;
-    const int base = consec ? wv * RPW : wv, step = consec ? 1 : TW;
+    const bool consec = PAIR || (RPW & 1) != 0;
+    const int base = PAIR ? ((int)blockIdx.x * H + wi % H) * RPW : (consec ? wv * RPW : wv), step = consec ? 1 : TW;
     const int real_rows = base < N ? min((N - 1 - base) / step + 1, RPW) : 0;
-    const int U_real = real_rows * KCH * PH;
-    int lq = 0, lk = 0, lp = 0, lt = 0;
-    bool lup = false;  // the unit last issued reads the up planes
+    const int U_real = real_rows * KCH;
+    int lq = 0, lk = 0, lt = 0;
+    const bool lup = upw;  // the units read the up planes
     uint32_t last = (uint32_t)min(base, N - 1) * (uint32_t)G + (uint32_t)lane;
     auto next_base = [&]() -> uint32_t {
         if (lt >= U_real) return last;
         const int row = base + lq * step;
         last = (uint32_t)row * (uint32_t)G + (uint32_t)(lk * CH + lane);
-        lup = PAIR && lp == 1;
         ++lt;
         if (++lk == KCH) {
             lk = 0;
-            if (PAIR && lp == 0) {
-                lp = 1;
-            } else {
-                lp = 0;
-                ++lq;
-            }
+            ++lq;
         }
         return last;
     };
@@ -671,13 +673,10 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     }
     __syncthreads();
 
-    float acc[MT], acc2[MT], res[MT], resg[PAIR ? MT : 1];
+    float acc[MT], acc2[MT], res[MT];
 #pragma unroll
-    for (int m = 0; m < MT; m++) {
-        acc[m] = acc2[m] = res[m] = 0.0f;
-        resg[PAIR ? m : 0] = 0.0f;
-    }
-    int cq = 0, ck = 0, cp = 0;  // compute-stream position (row ordinal, chunk, pass)
+    for (int m = 0; m < MT; m++) acc[m] = acc2[m] = res[m] = 0.0f;
+    int cq = 0, ck = 0;  // compute-stream position (row ordinal, chunk)
 
     // HOIST (a row is one K-chunk): every unit uses the same blocks, so the
     // activation operands are read from LDS once, before the loop.
@@ -738,22 +737,15 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
         }
         if (++ck == KCH) {
             // row done: reduce across the wave (fixed order), park it in lane cq
-            // (PAIR: the gate pass in resg, the up pass in res)
 #pragma unroll
             for (int m = 0; m < MT; m++) {
                 float v = wave_sum(acc[m]);
                 if (FMT == SLLM_Q5K1) v = v + wave_sum(acc2[m]);
-                if (PAIR && cp == 0) resg[PAIR ? m : 0] = (lane == cq) ? v : resg[PAIR ? m : 0];
-                else res[m] = (lane == cq) ? v : res[m];
+                res[m] = (lane == cq) ? v : res[m];
                 acc[m] = acc2[m] = 0.0f;
             }
             ck = 0;
-            if (PAIR && cp == 0) {
-                cp = 1;
-            } else {
-                cp = 0;
-                ++cq;
-            }
+            ++cq;
         }
     };
 
@@ -780,17 +772,43 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
         if (d < rem) compute(buf[d]);
 
     const int row = base + lane * step;  // lane q holds the sum of row ordinal q
+    if constexpr (PAIR) {
+        // the up waves hand their sums to the gate waves of the same rows; the
+        // gate waves form the gate part of the SwiGLU while they wait
+        __shared__ float ups[8][64][4];  // [gate wave][row ordinal][activation row]
+        float t[MT];
+#pragma unroll
+        for (int m = 0; m < MT; m++) t[m] = 0.0f;
+        if (upw && lane < real_rows) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) ups[wi - H][lane][m] = res[m];
+        } else if (!upw && lane < real_rows) {
+#pragma unroll
+            for (int m = 0; m < MT; m++)
+                if (m < M) t[m] = swiglu_gate(res[m]);
+        }
+        __syncthreads();
+        if (lane < real_rows) {
+#pragma unroll
+            for (int m = 0; m < MT; m++) {
+                if (m >= M) continue;
+                const size_t o = (size_t)m * N + row;
+                if (!upw) {
+                    dst[o] = t[m] * ups[wi][lane][m];  // swiglu(gate, up)
+                    if (S.dst[1]) S.dst[1][o] = res[m];
+                } else if (S.dst[2]) {
+                    S.dst[2][o] = res[m];
+                }
+            }
+        }
+        return;
+    }
     if (lane < real_rows) {
 #pragma unroll
         for (int m = 0; m < MT; m++) {
             if (m >= M) continue;
             const size_t o = (size_t)m * N + row;
-            if (PAIR) {
-                const float g = resg[PAIR ? m : 0], u = res[m];
-                dst[o] = swiglu(g, u);
-                if (S.dst[1]) S.dst[1][o] = g;
-                if (S.dst[2]) S.dst[2][o] = u;
-            } else if (dst) {
+            if (dst) {
                 // model_f32.go:472-474 / 495-497: x[i] += o[i], one float32 add
                 dst[o] = S.accum ? pre[m] + res[m] : res[m];
             }
@@ -814,7 +832,7 @@ sllm_status launch_t(const SegTable &S, const float *x, int G, int M, int KCH, i
     // o 5.23 -> 5.03 µs, RMSNorm + head + argmax 87.5 -> 87.0, C1 / C2 shapes
     // 5-15 % faster; 4 lanes for the fused gate + up (7 units per wave) cost it
     // 0.1 µs
-    int tpb = (S.norm_w || RPW * KCH * (PAIR ? 2 : 1) <= 2) ? 4 : 8;
+    int tpb = (S.norm_w || RPW * KCH <= 2) ? 4 : 8;
     while (tpb > (S.norm_w ? 4 : 1) && (int64_t)M * G * tpb > W * 64) tpb >>= 1;
     const bool hoist = kCanHoist && KCH == 1;
     if (S.norm_w) {
