@@ -218,9 +218,10 @@ sllm_status sllm_matmul_multi_dev(const sllm_weight *const *ws, int count, const
  * forwardBlock's FFN input in one call (model_f32.go:479-490): gate = Wgate x,
  * up = Wup x (modelMatmulIntoF32 on b.ffnNormed) and then, elementwise,
  * h = gate * float32(1 / (1 + exp(-float64(gate)))) * up, the reference's
- * SwiGLU loop in its operation order. h receives x_rows x Rows floats. For
- * decode (x_rows < 64) and weights of one QType this is a single GEMV launch
- * that streams each gate row and up row in the same wave and writes h
+ * SwiGLU loop in its operation order. h receives x_rows x Rows floats. Below
+ * the GEMM's row threshold (gemm_min_rows) and for weights of one QType this
+ * is a single GEMV launch (half of each workgroup's waves stream gate rows,
+ * the other half the same rows of up, and they meet in LDS) that writes h
  * directly; gate and up are not written unless gate_dev / up_dev are given
  * (each may be NULL). Wgate and Wup must have the same Rows and Cols == x_cols.
  */
