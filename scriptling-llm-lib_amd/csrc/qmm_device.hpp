@@ -289,8 +289,19 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
 // rounding per step) that are added at the end - about 2 VALU operations per
 // weight instead of 3, the two chains overlapping. The products v * x are
 // the reference's; only the order of the additions and their rounding differ
-// (each partial is within a few ulp of the block's sum |v x|).
-__device__ __forceinline__ float q5_block_sum_fma(int4 q, uint32_t qh, const float4 *xb) {
+// (each partial is within a few ulp of the block's sum |v x|). The codes are
+// q5_codes', with their high-bit half read from a table in LDS: entry t (16 B
+// apart, so the 16 entries sit in distinct banks) holds 0xf0 in byte k where
+// bit k of t is clear, and a group's entry is addressed by its four qh bits
+// times 16 (two operations and a read per four codes, where the multiply-
+// spread took five: C4 Q5_0 14336x4096 at M = 1 13.4-13.5 -> 12.1-12.2 us).
+__device__ __forceinline__ uint32_t q5_hi_mask(uint32_t t) {
+    uint32_t m = 0;
+    for (int k = 0; k < 4; k++)
+        if (!((t >> k) & 1u)) m |= 0xf0u << (8 * k);
+    return m;
+}
+__device__ __forceinline__ float q5_block_sum_tab(int4 q, uint32_t qh, const float4 *xb, const unsigned char *tab) {
     const uint32_t w[4] = {(uint32_t)q.x, (uint32_t)q.y, (uint32_t)q.z, (uint32_t)q.w};
     float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
@@ -299,8 +310,11 @@ __device__ __forceinline__ float q5_block_sum_fma(int4 q, uint32_t qh, const flo
         float4 b = xb[jj + 4];
         const float av[4] = {a.x, a.y, a.z, a.w};
         const float bv[4] = {b.x, b.y, b.z, b.w};
-        const uint32_t lo = q5_codes(w[jj], ~qh >> (4 * jj));
-        const uint32_t hi = q5_codes(w[jj] >> 4, ~qh >> (16 + 4 * jj));
+        // byte offsets 16 * (four qh bits) of elements 4jj.. and 16 + 4jj..
+        const uint32_t ol = jj == 1 ? (qh & 0xf0u) : (jj == 0 ? (qh << 4) : (qh >> (4 * jj - 4))) & 0xf0u;
+        const uint32_t oh = (qh >> (12 + 4 * jj)) & 0xf0u;
+        const uint32_t lo = (w[jj] & 0x0f0f0f0fu) | *(const uint32_t *)(tab + ol);
+        const uint32_t hi = ((w[jj] >> 4) & 0x0f0f0f0fu) | *(const uint32_t *)(tab + oh);
 #pragma unroll
         for (int k = 0; k < 4; k++) {
             s0 = __builtin_fmaf((float)(int)(int8_t)((lo >> (8 * k)) & 0xffu), av[k], s0);

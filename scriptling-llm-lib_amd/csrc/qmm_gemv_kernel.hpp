@@ -192,7 +192,8 @@ __device__ __forceinline__ float elem(const float4 *v, int e) {
 }
 
 template <int FMT>
-__device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x, float &acc, float &acc2) {
+__device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x, float &acc, float &acc2,
+                                           const unsigned char *q5tab = nullptr) {
     if (FMT == SLLM_Q2K) {
         // dequantizeQ2KNative (kquants.go:147-180) gives w = float32(d*sc*q -
         // dmin*m); here both products are exact in float32 and the difference
@@ -299,7 +300,7 @@ __device__ __forceinline__ void block_term(const BlockRegs &b, const ActRegs &x,
         t = t * x.xs;
         acc = acc + t;
     } else if (FMT == SLLM_Q5_0) {
-        const float sum = q5_block_sum_fma(b.q, b.qh, x.xf);
+        const float sum = q5_block_sum_tab(b.q, b.qh, x.xf, q5tab);
         const float grp = f16_lut(b.d) * sum;  // float32_ops.go:366 `s * sum`
         acc = acc + grp;
     } else if (FMT == SLLM_Q8_0) {
@@ -652,6 +653,13 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
     }
     __builtin_amdgcn_sched_barrier(0);
 
+    // Q5_0: the high-bit table of q5_block_sum_tab (16 entries, 16 B apart),
+    // written before the prologue's barrier
+    __shared__ __attribute__((aligned(16))) unsigned char q5tab_lds[FMT == SLLM_Q5_0 ? 256 : 16];
+    const unsigned char *q5tab = q5tab_lds;
+    if constexpr (FMT == SLLM_Q5_0) {
+        if (threadIdx.x < 16) *(uint32_t *)(q5tab_lds + 16 * threadIdx.x) = q5_hi_mask(threadIdx.x);
+    }
     BlockRegs buf[D][NB];
     // Prologue: the activation rows (M x G blocks) are quantized by all
     // threads, TPB lanes per block. Each thread issues its activation loads
@@ -714,11 +722,11 @@ __global__ void __launch_bounds__(1024) gemv_kernel(SegTable S, const float *__r
         for (int m = 0; m < MT; m++) {
             if (m >= M) continue;
             if (HOIST) {
-                block_term<FMT>(b, xh[HOIST ? i : 0][HOIST ? m : 0], acc[m], acc2[m]);
+                block_term<FMT>(b, xh[HOIST ? i : 0][HOIST ? m : 0], acc[m], acc2[m], q5tab);
             } else {
                 ActRegs xa;
                 load_act<FMT>(A, (size_t)m * G + g, xa);
-                block_term<FMT>(b, xa, acc[m], acc2[m]);
+                block_term<FMT>(b, xa, acc[m], acc2[m], q5tab);
             }
         }
     };
