@@ -293,8 +293,9 @@ __device__ __forceinline__ float q5_block_sum(int4 q, uint32_t qh, const float4 
 // q5_codes', with their high-bit half read from a table in LDS: entry t (16 B
 // apart, so the 16 entries sit in distinct banks) holds 0xf0 in byte k where
 // bit k of t is clear, and a group's entry is addressed by its four qh bits
-// times 16 (two operations and a read per four codes, where the multiply-
-// spread took five: C4 Q5_0 14336x4096 at M = 1 13.4-13.5 -> 12.1-12.2 us).
+// times 16 (about three operations and a read per four codes, where the
+// multiply-spread took six: C4 Q5_0 14336x4096 at M = 1 13.4-13.5 -> 12.1-12.2
+// us).
 __device__ __forceinline__ uint32_t q5_hi_mask(uint32_t t) {
     uint32_t m = 0;
     for (int k = 0; k < 4; k++)
