@@ -66,9 +66,10 @@ def test_shape_and_split_overrides(qtype, shape, splits):
     assert_fp32_parity(got.reshape(M, N), ref, term_abs_sum(qtype, raw, N, x), f"{qtype} shape={shape} S={splits}")
 
 
+@pytest.mark.parametrize("qtype", ["q8", "q5"])
 @pytest.mark.parametrize("splits", [9, 12, 16])
 @pytest.mark.parametrize("N,M", [(256, 64), (255, 65)])
-def test_split_reduction_layouts(splits, N, M):
+def test_split_reduction_layouts(qtype, splits, N, M):
     # the split reduction adds the partial tiles in split order whether it
     # moves four floats per thread (element count a multiple of 4, output
     # 16-byte aligned) or one (odd count, or an output 4 bytes off alignment),
@@ -76,7 +77,7 @@ def test_split_reduction_layouts(splits, N, M):
     # within the bound of the oracle's result
     import torch
 
-    qtype, K = "q8", 4096
+    K = 4096
     raw = make_raw(qtype, N, K, seed=splits + N)
     x = make_x(M, K, seed=splits)
     w = sq.DeviceWeight.from_quant(sq.QuantWeight(qtype, raw, K // 32, N, K))
