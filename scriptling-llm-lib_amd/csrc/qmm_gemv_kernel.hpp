@@ -410,10 +410,13 @@ __device__ __forceinline__ float rms_finish(const float *__restrict__ xr, int K,
     if (t < 256 && (t & 63) == 0) red[t >> 6] = w;
     __syncthreads();
     const float ss = ((red[0] + red[1]) + red[2]) + red[3];
-    const double ms = (double)ss / (double)K + (double)eps;
-    const float inv = 1.0f / (float)sqrt(ms);
-    __syncthreads();  // red may be reused
-    return inv;
+    // float64(ss) / float64(K): for a power-of-two K the quotient is exact, and
+    // so is the product with the exact reciprocal, without the division's
+    // iterations. red is written once per launch by each caller, so no barrier
+    // guards it after these reads.
+    const double q = (K & (K - 1)) == 0 ? (double)ss * (1.0 / (double)K) : (double)ss / (double)K;
+    const double ms = q + (double)eps;
+    return 1.0f / (float)sqrt(ms);
 }
 template <int RB = 16>
 __device__ __forceinline__ float rms_inv(const float *__restrict__ xr, int K, float eps, float *red) {
