@@ -82,6 +82,29 @@ def test_swiglu_row_counts(N, M):
     assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("knob,value", [("gemv_waves", 4), ("gemv_waves", 8), ("gemv_wg_per_cu", 2)])
+def test_swiglu_launch_shapes(knob, value):
+    # other workgroup shapes of the paired launch (2 or 4 gate waves and as many
+    # up waves per workgroup, two workgroups per CU): the same bits
+    N, K, M = 4501, 1024, 2
+    _, wg = _w("q4_1", N, K, seed=11)
+    _, wu = _w("q4_1", N, K, seed=12)
+    x = make_x(M, K, seed=13)
+    xd = torch.from_numpy(x).cuda()
+    h, g1, u1 = (torch.empty(M * N, device="cuda") for _ in range(3))
+    s = torch.cuda.current_stream().cuda_stream
+    sq.matmul_dev(wg, xd.data_ptr(), M, K, g1.data_ptr(), s)
+    sq.matmul_dev(wu, xd.data_ptr(), M, K, u1.data_ptr(), s)
+    sq.set_param(knob, value)
+    try:
+        sq.matmul_swiglu_dev(wg, wu, xd.data_ptr(), M, K, h.data_ptr(), stream=s)
+        torch.cuda.synchronize()
+    finally:
+        sq.set_param(knob, 16 if knob == "gemv_waves" else 1)
+    want = oracle.swiglu(g1.cpu().numpy(), u1.cpu().numpy())
+    assert np.array_equal(h.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def test_swiglu_host_entry_equals_device():
     N, K, M = 256, 1024, 2
     _, wg = _w("q4_1", N, K, seed=1)
