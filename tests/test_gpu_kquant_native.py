@@ -91,6 +91,31 @@ def test_block_sums_bit_exact_special_scales(t):
     assert np.array_equal(got[~gn].view(np.uint32), want[~wn].view(np.uint32))
 
 
+def test_q2k_block_sums_bit_exact_at_the_ends_of_the_f16_range():
+    # d and dmin from opposite ends of the f16 range (largest normals against
+    # subnormals, both ways, both signs): the GPU's one-rounding rebuild of
+    # d*sc*q - dmin*m must give the reference's float32 of its float64
+    # difference where the two products' magnitudes are furthest apart
+    N, K, M = 64, 1024, 2
+    raw = make_kq(10, N, K, 6).reshape(-1, PER[10])
+    rng = np.random.default_rng(7)
+    for i in range(raw.shape[0]):
+        big, small = int(rng.integers(0x7000, 0x7C00)), int(rng.integers(0x0001, 0x0400))
+        db, mb = (big, small) if i % 2 == 0 else (small, big)
+        db |= int(rng.integers(0, 2)) << 15
+        mb |= int(rng.integers(0, 2)) << 15
+        raw[i, 80:82] = [db & 0xFF, db >> 8]
+        raw[i, 82:84] = [mb & 0xFF, mb >> 8]
+    raw = raw.reshape(-1)
+    w = sq.load_weight_f32_direct(10, raw, N, K)
+    W = oracle.dense_weights(10, raw, N, K)
+    assert np.all(np.isfinite(W))
+    x = make_x(M, K, seed=8)
+    got = sq.debug_block_dots(w, x).view(np.float32)
+    want = oracle.dense_block_sums(W, x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
 @pytest.mark.parametrize("t,N,K,M", [(10, 300, 4096, 1), (11, 300, 4096, 1), (10, 96, 2048, 3),
                                      (11, 64, 1024, 70), (10, 14336, 4096, 1), (11, 4096, 14336, 1)])
 def test_matmul_within_reassociation_bound(t, N, K, M):

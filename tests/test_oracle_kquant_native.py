@@ -128,3 +128,88 @@ def test_dense_weights_are_the_float32_rounding():
     w = oracle.dense_weights(10, raw, 2, 512)
     assert w.dtype == np.float32 and w.shape == (2, 512)
     assert np.array_equal(w.reshape(-1), oracle.dequant("q2_k", raw, 1024).astype(np.float32))
+
+
+def _round_f32(fr) -> float:
+    """Correctly rounded float32 (nearest, ties to even) of an exact nonzero
+    rational in float32's normal range, by integer arithmetic."""
+    from fractions import Fraction
+    sign = -1.0 if fr < 0 else 1.0
+    a = abs(fr)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if a < Fraction(2) ** e:
+        e -= 1
+    elif a >= Fraction(2) ** (e + 1):
+        e += 1
+    scaled = a / Fraction(2) ** (e - 23)  # in [2^23, 2^24)
+    q, r = divmod(scaled.numerator, scaled.denominator)
+    if 2 * r > scaled.denominator or (2 * r == scaled.denominator and q & 1):
+        q += 1
+    return sign * q * 2.0 ** (e - 23)
+
+
+def test_q2k_fp64_difference_rounds_like_one_float32_rounding():
+    # The reference forms d*sc*q - dmin*m in float64 and the dense loader
+    # rounds it to float32 (kquants.go:163-172, gguf.go:907-911); the GPU
+    # rounds the exact difference once (a fused multiply-add: d*sc*q has at
+    # most 17 significant bits, dmin*m at most 15, both exact in float32).
+    # Both operands are integer multiples of 2^-24 (f16's finest step) below
+    # 2^22, so the float64 difference is always exact and the two routes
+    # round the same value once. Checked against exact rational arithmetic
+    # over scales from the ends of the f16 range, with float32 roundings that
+    # are inexact, also just below powers of two (where float32's spacing
+    # halves).
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    classes = []
+    for i in range(240):
+        kind = i % 4
+        if kind == 0:    # large d, subnormal dmin
+            db, mb = int(rng.integers(0x7000, 0x7C00)), int(rng.integers(0x0001, 0x0400))
+        elif kind == 1:  # subnormal d, large dmin
+            db, mb = int(rng.integers(0x0001, 0x0400)), int(rng.integers(0x7000, 0x7C00))
+        elif kind == 2:  # d a power of two, dmin tiny and positive
+            db, mb = int(rng.integers(0x18, 0x1F)) << 10, int(rng.integers(0x0001, 0x0100))
+        else:            # anywhere in the finite f16 range
+            db, mb = int(rng.integers(0x0001, 0x7C00)), int(rng.integers(0x0001, 0x7C00))
+        if kind != 2:
+            db |= int(rng.integers(0, 2)) << 15
+            mb |= int(rng.integers(0, 2)) << 15
+        classes.append((db, mb))
+    f16 = lambda b: float(np.array(b, np.uint16).view(np.float16))
+    blocks, expect = [], []
+    for db, mb in classes:
+        codes = rng.integers(0, 4, 256)
+        sc = rng.integers(0, 16, 16)
+        mn = rng.integers(0, 16, 16)
+        if db & 0x3FF == 0:  # scales 1, 2, 4, 8 (and codes 1, 2) keep d*sc*q a power of two
+            sc = np.array([1, 2, 4, 8])[rng.integers(0, 4, 16)]
+        d, dm = f16(db), f16(mb)
+        blocks.append(encode_q2k(codes, sc, mn, d, dm))
+        expect.append((d, dm, codes, sc, mn))
+    raw = np.concatenate(blocks)
+    got = oracle.dequant("q2_k", raw, 256 * len(blocks)).astype(np.float32).reshape(len(blocks), 256)
+    inexact64 = inexact32 = pow2_inexact = 0
+    for bi, (d, dm, codes, sc, mn) in enumerate(expect):
+        memo = {}
+        for e in range(256):
+            key = (int(sc[e // 16]), int(codes[e]), int(mn[e // 16]))
+            if key not in memo:
+                s, q, m = key
+                exact = Fraction(d) * s * q - Fraction(dm) * m
+                if exact == 0:
+                    memo[key] = None
+                else:
+                    memo[key] = _round_f32(exact)
+                    inexact64 += int(Fraction(float(np.float64(d * s * q) - np.float64(dm * m))) != exact)
+                    if Fraction(memo[key]) != exact:
+                        inexact32 += 1
+                        pow2_inexact += int(d * s * q > 0 and (d * s * q).hex().startswith("0x1.0000000000000p"))
+            want = memo[key]
+            if want is None:
+                assert got[bi, e] == 0.0
+            else:
+                assert np.float32(want).view(np.uint32) == got[bi, e].view(np.uint32), (bi, e, key)
+    assert inexact64 == 0      # the float64 difference never rounds
+    assert inexact32 > 1000    # the float32 rounding does
+    assert pow2_inexact > 10   # ... also just below powers of two
